@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Routed SpMM benchmark on one MI355X (driver contract: one JSON line on stdout).
+
+Default workload = BASELINE config 2: Chung-Lu power-law graph (M = 1e6, mean
+degree 16, gamma 2.1, hubs), GCN-normalised fp32 values, dense B of 1e6 x 128
+fp32 N(0,1) (synthetic, seeded), C = A @ B through the MI355X router.
+
+  step      one routed SpMM over the whole matrix (plan built outside the timed
+            region, inputs resident in HBM)
+  value     warm GFLOP/s = 2 * nnz * N / (seconds per step)
+  roofline  dominant kernel: algorithmic bytes per launch / its mean launch
+            time from HIP events on the launch stream, against 8 TB/s
+  cold      routing (GPU feature pass + decision) and plan build + first
+            execution, each the mean of 10 repetitions
+  cpu       oracle/spmm_oracle.c sequential fma on one host core (kind "port")
+            and torch.sparse CSR on all host threads, same matrix
+
+Other configurations: --config C1..C5 (parity-size workloads; not the driver
+line).  --sweep times every deployed path on the chosen configs (calibration).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "ra-spmm_amd", ROOT):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "SpMM GFLOP/s (2*nnz*N) + % HBM roofline, warm and cold, N=128, 1 MI355X"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bytes_alg(M, K, nnz, N, s_val=4, s_b=4, s_c=4):
+    """Compulsory traffic: rowptr + (colind, vals) + B once + C once."""
+    return 4 * (M + 1) + nnz * (4 + s_val) + K * N * s_b + M * N * s_c
+
+
+def bytes_edgewise(M, nnz, N):
+    """Reference byte model 12*nnz + 4*nnz*N + 4*M*N (ra_eval_utils.py:647-651)."""
+    return 12 * nnz + 4 * nnz * N + 4 * M * N
+
+
+def timed_steps(fn, steps, warmup):
+    """W untimed steps, then exactly K steps bracketed by synchronize; returns
+    (wall ms per step, event ms per step)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        fn()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, ev0.elapsed_time(ev1) / steps
+
+
+def cpu_baselines(g, N, seconds=12.0):
+    """Oracle sequential fma (1 core) and torch.sparse CSR (all threads)."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    O.build()
+    rng = np.random.default_rng(7)
+    B = rng.standard_normal((g.K, N)).astype(np.float32)
+    flops = 2.0 * g.nnz * N
+    reps, t_tot = 0, 0.0
+    while t_tot < seconds and reps < 20:
+        t0 = time.perf_counter()
+        O.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
+        t_tot += time.perf_counter() - t0
+        reps += 1
+    port = {"value": flops * reps / t_tot / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"full matrix (M={g.M}, nnz={g.nnz}, N={N}) x {reps} repetitions, "
+                      f"oracle/spmm_oracle.c sequential fma, 1 thread, {t_tot:.1f} s"}
+    A = torch.sparse_csr_tensor(torch.from_numpy(g.rowptr.astype(np.int64)),
+                                torch.from_numpy(g.colind.astype(np.int64)),
+                                torch.from_numpy(g.vals), size=(g.M, g.K))
+    Bt = torch.from_numpy(B)
+    torch.sparse.mm(A, Bt)  # warm
+    reps, t_tot = 0, 0.0
+    while t_tot < seconds / 2 and reps < 20:
+        t0 = time.perf_counter()
+        torch.sparse.mm(A, Bt)
+        t_tot += time.perf_counter() - t0
+        reps += 1
+    ts = {"value": flops * reps / t_tot / 1e9, "unit": "GFLOP/s",
+          "threads": torch.get_num_threads(), "affinity_cores": len(os.sched_getaffinity(0)),
+          "sample": f"full matrix x {reps} repetitions, torch.sparse.mm on a CPU CSR tensor"}
+    return port, ts
+
+
+def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
+    """Mean launch time of the dominant kernel of `label`, HIP events on the
+    current stream (the stream every ra_spmm launch uses)."""
+    import torch
+    import ra_spmm
+    if label == "ZERO_OVERHEAD_CSR":
+        C = torch.empty(rp.numel() - 1, B.shape[1], device=B.device)
+        fn = lambda: ra_spmm._C.run_zero_overhead_plan_stage(plan, rp, ci, vl, B, C, 1)  # noqa: E731
+        name = "zo_fused_kernel"
+    elif label == "CSR_DIRECT":
+        fn = lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B)  # noqa: E731
+        name = "csr_rows_kernel"
+    else:
+        fn = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
+        name = "tile kernels (path total)"
+    _, ev = timed_steps(fn, steps, 5)
+    return ev, name
+
+
+def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10):
+    import numpy as np
+    import torch
+    import ra_spmm
+    from ra_spmm import synthetic as S
+
+    t0 = time.perf_counter()
+    g = S.CONFIGS[cfg]()
+    log(f"[bench] {cfg}: {g.name} M={g.M} nnz={g.nnz} generated in {time.perf_counter() - t0:.1f} s")
+    rp, ci, vl = g.torch("cuda")
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    B = torch.randn(g.K, N, device="cuda", generator=gen)
+    torch.cuda.synchronize()
+
+    # Cold part (i): routing = GPU feature pass + rule tree.
+    route_ms = []
+    for _ in range(cold_reps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        plan_dict = ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N, "MAIN", table)
+        route_ms.append((time.perf_counter() - t) * 1e3)
+    label = ra_spmm.route_label(plan_dict)
+    log(f"[bench] routed to {label} ({plan_dict['decision_reason']}), "
+        f"d={plan_dict['feature_values']['avg_nnz_per_row']:.3f} "
+        f"cv={plan_dict['feature_values']['degree_cv']:.3f}")
+
+    # Cold part (ii): plan build + first execution.
+    rp_cpu, ci_cpu, vl_cpu = rp.cpu(), ci.cpu(), vl.cpu()
+    build_ms, first_ms = [], []
+    for _ in range(cold_reps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        plan = ra_spmm.build_kernel_plan(label, rp_cpu, ci_cpu, vl_cpu, g.M, g.K, N)
+        torch.cuda.synchronize()
+        build_ms.append((time.perf_counter() - t) * 1e3)
+        _, ms = ra_spmm.measure_one_ms(lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B))
+        first_ms.append(ms)
+
+    run = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
+    wall_ms, ev_ms = timed_steps(run, steps, warmup)
+    C = run()
+    flops = 2.0 * g.nnz * N
+    gflops = flops / (wall_ms * 1e-3) / 1e9
+    k_ms, k_name = kernel_time_ms(label, plan, rp, ci, vl, B, steps)
+    b_alg = bytes_alg(g.M, g.K, g.nnz, N)
+
+    # Comparators on the same inputs.
+    base_wall, base_ev = timed_steps(lambda: ra_spmm.spmm_csr_baseline(rp, ci, vl, B), max(20, steps // 4), 5)
+    cd_wall, cd_ev = timed_steps(lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B), max(20, steps // 4), 5)
+    C_base = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
+    scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
+    max_rel = float(((C - C_base).abs() / (scale + 1e-30)).max())
+
+    res = {
+        "config": cfg, "graph": g.name, "M": g.M, "K": g.K, "nnz": g.nnz, "N": N, "path": label,
+        "decision_reason": plan_dict["decision_reason"],
+        "avg_nnz_per_row": plan_dict["feature_values"]["avg_nnz_per_row"],
+        "degree_cv": plan_dict["feature_values"]["degree_cv"],
+        "ms_per_step": wall_ms, "event_ms_per_step": ev_ms, "gflops": gflops,
+        "kernel": k_name, "kernel_ms": k_ms, "bytes_alg": b_alg,
+        "bytes_edgewise": bytes_edgewise(g.M, g.nnz, N),
+        "cold_route_ms": sum(route_ms) / len(route_ms),
+        "cold_build_ms": sum(build_ms) / len(build_ms),
+        "cold_first_exec_ms": sum(first_ms) / len(first_ms),
+        "baseline_ms": base_wall, "baseline_gflops": flops / (base_wall * 1e-3) / 1e9,
+        "csr_direct_ms": cd_wall, "csr_direct_gflops": flops / (cd_wall * 1e-3) / 1e9,
+        "speedup_vs_baseline": base_wall / wall_ms,
+        "max_rel_err_vs_baseline": max_rel,
+    }
+    if do_cpu:
+        port, ts = cpu_baselines(g, N)
+        res["cpu_port"] = port
+        res["cpu_torch_sparse"] = ts
+    return res
+
+
+def sweep(configs, Ns, steps, out_path):
+    """Every deployed path on each config (calibration of the MI355X table)."""
+    import torch
+    import ra_spmm
+    from ra_spmm import synthetic as S
+    rows = []
+    for cfg in configs:
+        g = S.CONFIGS[cfg]()
+        rp, ci, vl = g.torch("cuda")
+        for N in Ns:
+            B = torch.randn(g.K, N, device="cuda")
+            base = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
+            scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
+            for label in ["CSR_BASELINE"] + ra_spmm.DEPLOYED_KERNELS:
+                if label in ra_spmm.TILE_KERNELS and N < 16:
+                    continue
+                t = time.perf_counter()
+                plan = ra_spmm.build_kernel_plan(label, rp.cpu(), ci.cpu(), vl.cpu(), g.M, g.K, N)
+                torch.cuda.synchronize()
+                build = (time.perf_counter() - t) * 1e3
+                fn = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
+                wall, ev = timed_steps(fn, steps, 3)
+                err = float(((fn() - base).abs() / (scale + 1e-30)).max())
+                row = {"config": cfg, "N": N, "path": label, "ms": wall, "event_ms": ev,
+                       "gflops": 2.0 * g.nnz * N / (wall * 1e-3) / 1e9, "build_ms": build,
+                       "max_rel_err_vs_baseline": err}
+                rows.append(row)
+                log(f"[sweep] {cfg} N={N:4d} {label:22s} {wall:9.3f} ms {row['gflops']:9.1f} GF/s "
+                    f"build {build:8.1f} ms err {err:.2e}")
+                del plan
+            del B
+        del rp, ci, vl
+        torch.cuda.empty_cache()
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps(rows, indent=1))
+    return rows
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--N", type=int, default=128)
+    ap.add_argument("--table", default="mi355x", choices=["mi355x", "reference"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--traffic", type=float, default=None,
+                    help="HBM bytes per launch of the dominant kernel from rocprofv3 --pmc")
+    ap.add_argument("--sweep", default=None, help="comma-separated configs to sweep all paths on")
+    ap.add_argument("--sweep-N", default="64,128,256")
+    ap.add_argument("--sweep-out", default="gpurun_out/sweep.json")
+    ap.add_argument("--details", default=None, help="write the full result dict here")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              f"(the SpMM shards by row blocks, see the sharding notes; run with --gpus 1)",
+              file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 3
+    if args.sweep:
+        sweep(args.sweep.split(","), [int(n) for n in args.sweep_N.split(",")], max(10, args.steps // 4),
+              args.sweep_out)
+        return 0
+
+    res = bench_config(args.config, args.N, args.steps, args.warmup, args.table, not args.no_cpu)
+    achieved = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(res["gflops"], 3), "unit": "GFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded generator, ra_spmm.synthetic)",
+        "config": {"workload": f"{args.config} {res['graph']} M={res['M']} nnz={res['nnz']} "
+                               f"N={res['N']} fp32, routed ({res['path']})",
+                   "N": res["N"], "router_table": args.table},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": args.traffic, "kernel": res["kernel"],
+                     "kernel_ms": round(res["kernel_ms"], 5), "bytes_alg": res["bytes_alg"]},
+        "cpu_baseline": res.get("cpu_port"),
+        "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
+                 "first_exec_ms": round(res["cold_first_exec_ms"], 4)},
+        "path": res["path"],
+        "baseline_csr_gflops": round(res["baseline_gflops"], 3),
+        "csr_direct_gflops": round(res["csr_direct_gflops"], 3),
+        "speedup_vs_baseline_kernel": round(res["speedup_vs_baseline"], 4),
+        "edgewise_gbs": round(res["bytes_edgewise"] / (res["ms_per_step"] * 1e-3) / 1e9, 1),
+        "max_rel_err_vs_baseline": res["max_rel_err_vs_baseline"],
+        "cpu_torch_sparse": res.get("cpu_torch_sparse"),
+    }
+    if args.details:
+        Path(args.details).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.details).write_text(json.dumps(res, indent=1))
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

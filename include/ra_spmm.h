@@ -1,0 +1,289 @@
+/*
+ * ra_spmm.h — C ABI of the MI355X-native regime-aware SpMM engine.
+ *
+ * C = A * B with A an M x K CSR matrix (int32 rowptr/colind, fp32 values) and
+ * B a dense K x N row-major matrix; C is dense M x N row-major fp32.
+ *
+ * Conventions
+ *   - Pointers named d_* are device (HBM) pointers, h_* are host pointers.
+ *   - Every kernel entry point is asynchronous on `stream` (a hipStream_t;
+ *     NULL = the null stream) and writes EVERY element of C, so C may be
+ *     uninitialised on entry.
+ *   - Functions return ra_status; on failure ra_last_error() holds a
+ *     thread-local, human-readable message.  No function throws.
+ *   - Plan handles are opaque, owned by the caller, released with the
+ *     matching *_destroy.  A plan keeps per-plan scratch, so one plan must not
+ *     be run concurrently from two streams.
+ *
+ * Each declaration names the reference interface it replaces
+ * (tariqaf/RA-SpMM, file:line).
+ */
+#ifndef RA_SPMM_H
+#define RA_SPMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RA_SPMM_ABI_VERSION 1
+
+/* Opaque stream handle: identical to hipStream_t (struct ihipStream_t*). */
+typedef struct ihipStream_t* ra_stream_t;
+
+typedef enum ra_status {
+    RA_OK = 0,
+    RA_ERR_INVALID_ARGUMENT = 1,
+    RA_ERR_HIP = 2,           /* a HIP runtime call failed                 */
+    RA_ERR_OUT_OF_MEMORY = 3,
+    RA_ERR_UNSUPPORTED = 4,   /* shape/dtype combination not implemented   */
+    RA_ERR_INACTIVE_PLAN = 5, /* tile plan built with N < 16               */
+    RA_ERR_INTERNAL = 6
+} ra_status;
+
+typedef enum ra_dtype {
+    RA_DTYPE_F32 = 0,
+    RA_DTYPE_F16 = 1,
+    RA_DTYPE_BF16 = 2
+} ra_dtype;
+
+/* Path ids keep the reference NextPath numbering (ra_common.h:76-95). */
+typedef enum ra_path {
+    RA_PATH_CSR_DIRECT = 0,
+    RA_PATH_CSR_ADAPTIVE = 1,
+    RA_PATH_STAGED_REUSE = 2,
+    RA_PATH_TC_SPARSE = 3,
+    RA_PATH_ROW_SPLIT_CUDA = 4,
+    RA_PATH_TC_REORDERED = 5,
+    RA_PATH_HYBRID_TC_CUDA = 6,
+    RA_PATH_CUSPARSE = 7,          /* served by the baseline CSR kernel */
+    RA_PATH_RODE_ENHANCED = 8,
+    RA_PATH_VECTORIZED_COARSE = 9,
+    RA_PATH_LOCALITY_TILED = 10,
+    RA_PATH_TC_DIRECT = 11,
+    RA_PATH_COMMUNITY_TC = 12,
+    RA_PATH_ZERO_OVERHEAD_CSR = 13,
+    RA_PATH_SEGMENT_HYBRID = 14,
+    RA_PATH_COUNT = 15
+} ra_path;
+
+/* Rejection codes keep the reference RejectReason numbering (ra_common.h:145-159). */
+typedef enum ra_reject {
+    RA_REJECT_CHOSEN = 0,
+    RA_REJECT_NOT_FEASIBLE = 1,
+    RA_REJECT_LOW_FILL = 2,
+    RA_REJECT_LOW_COVERAGE = 3,
+    RA_REJECT_HIGH_SKEW = 4,
+    RA_REJECT_SMALL_N = 5,
+    RA_REJECT_INSUFFICIENT_NNZ = 6,
+    RA_REJECT_LOW_OCCUPANCY = 7,
+    RA_REJECT_LOW_DEGREE_SKEW = 8,
+    RA_REJECT_NOT_STRONG_ENOUGH = 9,
+    RA_REJECT_MARGIN_TOO_SMALL = 10,
+    RA_REJECT_NOT_IN_PORTFOLIO = 11,
+    RA_REJECT_UNKNOWN = 12
+} ra_reject;
+
+typedef enum ra_portfolio { RA_PORTFOLIO_MAIN = 0, RA_PORTFOLIO_FULL = 1 } ra_portfolio;
+
+/* Threshold table of the seven-rule router. REFERENCE reproduces the
+ * published decisions; MI355X is recalibrated from measurements on gfx950. */
+typedef enum ra_router_table { RA_TABLE_REFERENCE = 0, RA_TABLE_MI355X = 1 } ra_router_table;
+
+/* Tile-route precision: FP16 / BF16 MFMA, or the FP32-FMA route that replaces
+ * the reference's TF32 path (gfx950 has no xf32 MFMA). */
+typedef enum ra_tile_route {
+    RA_TILE_ROUTE_F16 = 0,
+    RA_TILE_ROUTE_BF16 = 1,
+    RA_TILE_ROUTE_FP32 = 2
+} ra_tile_route;
+
+typedef enum ra_tile_kind {
+    RA_TILE_TC_DIRECT = 0,
+    RA_TILE_COMMUNITY_TC = 1,
+    RA_TILE_SEGMENT_HYBRID = 2
+} ra_tile_kind;
+
+/* ------------------------------------------------------------------ misc */
+int ra_abi_version(void);
+const char* ra_status_string(ra_status status);
+const char* ra_last_error(void);
+/* Reference: next_path_name, ra_common.h:116-135. */
+const char* ra_path_name(int32_t path);
+/* Reference: reject_reason_str, ra_common.h:161-178. */
+const char* ra_reject_name(int32_t code);
+
+/* -------------------------------------------------------------- features
+ * The four routing inputs from rowptr alone.  Both backends reduce the exact
+ * integers nnz, sum(deg^2) and max(deg) and share one finalisation, so the
+ * host and device paths produce bit-identical features.
+ * Reference: compute_production_router_features, router/router_features.cpp:79-111
+ *            compute_production_router_features_gpu, router/router_features_cuda.cu:51-92 */
+typedef struct ra_features {
+    int32_t M, K, N;
+    int32_t max_deg;
+    int64_t nnz;          /* rowptr[M] - rowptr[0]            */
+    int64_t sum_deg_sq;   /* exact sum of squared row lengths */
+    int64_t empty_rows;
+    double avg;           /* nnz / M                          */
+    double std_dev;       /* population std of row length     */
+    float avg_nnz_per_row;
+    float std_nnz_per_row;
+    float degree_cv;
+    float max_to_mean_ratio;
+} ra_features;
+
+ra_status ra_features_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_t N,
+                           ra_features* out);
+/* Synchronises `stream` (one 32-byte readback). */
+ra_status ra_features_device(const int32_t* d_rowptr, int32_t M, int32_t K, int32_t N,
+                             ra_stream_t stream, ra_features* out);
+/* Shared finalisation from exact integer moments. */
+ra_status ra_features_from_moments(int32_t M, int32_t K, int32_t N, int64_t nnz,
+                                   int64_t sum_deg_sq, int32_t max_deg, int64_t empty_rows,
+                                   ra_features* out);
+
+/* ---------------------------------------------------------------- router
+ * Reference: route_dispatch deployed block, router/router_dispatch.cpp:979-1110,
+ *            feasibility router/router_dispatch.cpp:107-464. */
+typedef struct ra_route {
+    int32_t chosen_path;      /* ra_path                               */
+    int32_t use_tf32;         /* run the tile path on its FP32 route   */
+    int32_t rule;             /* 1..7 = matched rule, 8 = fallthrough  */
+    int32_t tile_ok;
+    float estimated_risk;
+    float pad_;
+    double est_plan_s;        /* preprocessing-aware tile-gate estimate */
+    char decision_reason[64];
+    int8_t feasible[RA_PATH_COUNT];
+    int8_t rejection_code[RA_PATH_COUNT];
+} ra_route;
+
+ra_status ra_route_dispatch(const ra_features* features, int32_t portfolio, int32_t table,
+                            ra_route* out);
+
+/* ------------------------------------------------------------ CSR family */
+/* CSR_DIRECT: lane-group-per-row SpMM for 64-lane wavefronts.
+ * Reference: csr_direct_spmm, csr/csr_direct.cu:234-338 (binding spmm_csr_direct,
+ *            bindings/ra_bindings.cpp:724-742). */
+ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
+                             const float* d_vals, const float* d_B, float* d_C,
+                             int32_t M, int32_t K, int32_t N, int64_t nnz,
+                             ra_stream_t stream);
+
+/* Hand-written regime-free baseline CSR kernel (one row per wavefront).
+ * Replaces the cuSPARSE guardrail: CuSparseSpMMState, bindings/ra_bindings.cpp:431-615;
+ * spmm_cusparse_fn, bindings/ra_bindings.cpp:821-836. */
+ra_status ra_spmm_csr_baseline(const int32_t* d_rowptr, const int32_t* d_colind,
+                               const float* d_vals, const float* d_B, float* d_C,
+                               int32_t M, int32_t K, int32_t N, int64_t nnz,
+                               ra_stream_t stream);
+
+/* ZERO_OVERHEAD_CSR: O(M) degree binning, small-row lane groups, 256-nnz hub
+ * chunks with a deterministic merge.
+ * Reference: make_ra_zero_overhead_plan / run_ra_zero_overhead_plan,
+ *            csr/ra_zero_overhead.cu:312-506; RAZeroOverheadPlan, ra_common.h:507-530. */
+typedef struct ra_zo_plan ra_zo_plan;
+typedef struct ra_zo_info {
+    int32_t M, K;
+    int32_t num_tiny, num_short, num_medium, num_long, num_empty;
+    int32_t num_small;        /* tiny + short + medium                   */
+    int32_t num_chunks;       /* 256-nnz chunks of rows with > 64 nnz    */
+    int32_t num_sole_chunks;  /* rows of 65..256 nnz: one chunk, direct  */
+    int32_t num_split_rows;   /* rows of > 256 nnz                       */
+    int32_t num_split_chunks; /* their chunks (partial slots)            */
+    int32_t max_long_chunks;
+    int32_t pad_;
+    int64_t plan_bytes;
+} ra_zo_info;
+
+/* Host-only binning (no device work): fills the lists the plan uploads.
+ * small_rows: tiny, then short, then medium rows, each in ascending row order;
+ * chunk_rows/chunk_starts: one entry per 256-nnz chunk, bit 31 of chunk_rows set
+ * on sole chunks.  Any output pointer may be NULL; counts go to *info. */
+ra_status ra_zo_bins_host(const int32_t* h_rowptr, int32_t M, int32_t K,
+                          int32_t* small_rows, int32_t* chunk_rows, int32_t* chunk_starts,
+                          int32_t* empty_rows, ra_zo_info* info);
+ra_status ra_zo_plan_create(const int32_t* h_rowptr, int32_t M, int32_t K, ra_zo_plan** out);
+ra_status ra_zo_plan_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
+                         const float* d_vals, const float* d_B, float* d_C, int32_t N,
+                         ra_stream_t stream);
+/* Measurement hook (no reference counterpart): stage 1 runs only the fused
+ * chunk + short-row kernel, stage 2 only the deterministic merge of split rows,
+ * stage 0 both (== ra_zo_plan_run).  Lets a profiler time each launch alone. */
+ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
+                               const int32_t* d_colind, const float* d_vals, const float* d_B,
+                               float* d_C, int32_t N, int32_t stage, ra_stream_t stream);
+ra_status ra_zo_plan_get_info(const ra_zo_plan* plan, ra_zo_info* info);
+void ra_zo_plan_destroy(ra_zo_plan* plan);
+
+/* ----------------------------------------------------------- tile family
+ * 8-row windows; every distinct column of a window is an 8x1 vector; 8 vectors
+ * form a block (the last one zero-padded).  COMMUNITY_TC first stable-sorts rows
+ * by their leading column; SEGMENT_HYBRID splits windows with > 64 blocks into
+ * <= 64-block segments merged deterministically.
+ * Reference: build_ra_tc_direct_plan_impl, tc/ra_tc_direct.cu:627-780;
+ *            make_ra_community_tc_plan, tc/ra_community_tc.cu:320-471;
+ *            make_ra_segment_hybrid_plan, tc/ra_segment_hybrid.cu:371-543;
+ *            run_* of the three files (tc/ra_tc_direct.cu:805-894,
+ *            tc/ra_community_tc.cu:476-552, tc/ra_segment_hybrid.cu:548-668). */
+typedef struct ra_tile_host ra_tile_host;
+typedef struct ra_tile_plan ra_tile_plan;
+typedef struct ra_tile_info {
+    int32_t kind, M, K, active;
+    int32_t num_windows;
+    int32_t num_blocks;        /* reference num_tc_tiles                   */
+    int32_t num_segments;
+    int32_t num_split_windows;
+    int32_t num_split_segs;
+    int32_t max_window_blocks;
+    int64_t nnz;
+    int64_t num_vectors;       /* distinct (window, column) pairs          */
+    int64_t plan_bytes;
+    float avg_tile_density;    /* nnz / (8 * 8 * num_blocks)               */
+    int32_t value_dtype;       /* RA_DTYPE_F16 or RA_DTYPE_BF16            */
+    double build_ms;           /* host build + upload                      */
+} ra_tile_info;
+
+/* Host-only build of the tile format (testable without a GPU).
+ * value_dtype: RA_DTYPE_F16 or RA_DTYPE_BF16 (storage of the block values). */
+ra_status ra_tile_host_build(int32_t kind, const int32_t* h_rowptr, const int32_t* h_colind,
+                             const float* h_vals, int32_t M, int32_t K, int32_t N,
+                             int32_t value_dtype, ra_tile_host** out);
+ra_status ra_tile_host_get_info(const ra_tile_host* host, ra_tile_info* info);
+/* Array export for structural checks. name: "block_offsets", "atox", "win_rows",
+ * "vals" (uint16 bits, [block][row 8][vector 8]), "seg_window", "seg_bbegin",
+ * "seg_bend", "seg_slot", "split_windows", "split_offsets".
+ * Returns the element count in *count; copies when dst != NULL. */
+ra_status ra_tile_host_export(const ra_tile_host* host, const char* name, void* dst,
+                              int64_t* count);
+void ra_tile_host_destroy(ra_tile_host* host);
+
+ra_status ra_tile_plan_create(int32_t kind, const int32_t* h_rowptr, const int32_t* h_colind,
+                              const float* h_vals, int32_t M, int32_t K, int32_t N,
+                              int32_t value_dtype, ra_tile_plan** out);
+/* B fp32 [K,N]; route: ra_tile_route.  The FP16/BF16 routes convert B into
+ * plan scratch first (one extra pass over B). */
+ra_status ra_tile_plan_run(ra_tile_plan* plan, const float* d_B, float* d_C, int32_t N,
+                           int32_t route, ra_stream_t stream);
+/* B already fp16/bf16 with leading dimension ldb (elements, ldb >= N and a
+ * multiple of 8): no conversion pass. */
+ra_status ra_tile_plan_run_lowp(ra_tile_plan* plan, const void* d_Bh, int32_t ldb,
+                                int32_t b_dtype, float* d_C, int32_t N, ra_stream_t stream);
+ra_status ra_tile_plan_get_info(const ra_tile_plan* plan, ra_tile_info* info);
+void ra_tile_plan_destroy(ra_tile_plan* plan);
+
+/* ------------------------------------------------------------ utilities */
+/* fp32 -> fp16/bf16 round-to-nearest-even conversion of a [rows, cols] matrix
+ * into a buffer with leading dimension ldo (columns cols..ldo-1 zero-filled).
+ * Reference: convert_b_to_half_kernel, tc/ra_tc_direct.cu:85-104. */
+ra_status ra_convert_f32(const float* d_in, void* d_out, int64_t rows, int32_t cols,
+                         int32_t ldo, int32_t out_dtype, ra_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RA_SPMM_H */

@@ -1,0 +1,665 @@
+// csr_kernels.hip — CSR family on 64-lane wavefronts (gfx950).
+//
+//   CSR_DIRECT         a lane group of G lanes owns one row; each lane keeps V
+//                      packets (float4 when N % 4 == 0 and buffers are 16-byte
+//                      aligned, float otherwise) of the output row, so one
+//                      wave-wide dwordx4 load gathers 64/G whole B rows.
+//                      (col, val) of a G-wide slice of the row are loaded
+//                      coalesced, one per lane, and broadcast with ds_bpermute.
+//   baseline           regime-free reference point: one wave per row, lanes
+//                      stride over columns, scalar loads.
+//   ZERO_OVERHEAD_CSR  one fused launch: hub chunks (256 nnz) first, then the
+//                      degree-binned short rows; chunks of rows longer than 256
+//                      write fp32 partials that a second launch sums in
+//                      ascending chunk order (deterministic, no atomics).
+//   features           exact integer degree moments (nnz, sum d^2, max d,
+//                      empty rows) in two deterministic launches.
+//
+// Every output element of CSR_DIRECT, of the baseline and of short ZO rows is
+// one fp32 accumulator updated by fma in CSR order, which is bit-identical to
+// the reference per-lane accumulation (csr/csr_direct.cu:201-228).
+#include <algorithm>
+#include <mutex>
+
+#include "ra_internal.hpp"
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = kWave * kWavesPerBlock;
+
+// ZO bin thresholds (csr/ra_zero_overhead.cu:55-59).
+constexpr int kTiny = 4, kShort = 16, kMedium = 64, kChunk = 256;
+constexpr uint32_t kSoleFlag = 0x80000000u;
+
+// ------------------------------------------------------------------ packets
+template <typename P> __device__ __forceinline__ P pzero();
+template <> __device__ __forceinline__ float pzero<float>() { return 0.f; }
+template <> __device__ __forceinline__ float4 pzero<float4>() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+__device__ __forceinline__ float pfma(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ float4 pfma(float a, float4 b, float4 c) {
+    return make_float4(__builtin_fmaf(a, b.x, c.x), __builtin_fmaf(a, b.y, c.y),
+                       __builtin_fmaf(a, b.z, c.z), __builtin_fmaf(a, b.w, c.w));
+}
+__device__ __forceinline__ float padd(float a, float b) { return a + b; }
+__device__ __forceinline__ float4 padd(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// Accumulate the nnz range [p0, p1) of one row into acc.  All G lanes of the
+// group share the range; lane `sl` owns packet columns q[s] (q < 0: masked).
+// Per output element the update order is p ascending, one fma per nonzero.
+template <int G, int V, typename P>
+__device__ __forceinline__ void accumulate_range(const int32_t* __restrict__ colind,
+                                                 const float* __restrict__ vals,
+                                                 const P* __restrict__ Bp, int64_t ldp,
+                                                 int p0, int p1, int sl, const int (&q)[V],
+                                                 P (&acc)[V]) {
+    constexpr int U = (G >= 4) ? 4 : G;  // gathers in flight per lane
+    for (int base = p0; base < p1; base += G) {
+        const int my = base + sl;
+        int mc = 0;
+        float mv = 0.f;
+        if (my < p1) {
+            mc = colind[my];
+            mv = vals[my];
+        }
+        const int cnt = min(G, p1 - base);
+        for (int j = 0; j < cnt; j += U) {
+            int c[U];
+            float a[U];
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                c[k] = __shfl(mc, j + k, G);
+                a[k] = __shfl(mv, j + k, G);
+            }
+            P b[U][V];
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+#pragma unroll
+                for (int s = 0; s < V; ++s) {
+                    b[k][s] = (j + k < cnt && q[s] >= 0) ? Bp[(int64_t)c[k] * ldp + q[s]]
+                                                        : pzero<P>();
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                if (j + k < cnt) {
+#pragma unroll
+                    for (int s = 0; s < V; ++s) acc[s] = pfma(a[k], b[k][s], acc[s]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- CSR_DIRECT
+template <int G, int V, typename P>
+__global__ __launch_bounds__(kBlock) void csr_rows_kernel(
+    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
+    const float* __restrict__ vals, const P* __restrict__ Bp, P* __restrict__ Cp,
+    const int32_t* __restrict__ row_list, int64_t num_rows, int64_t ldp, int np) {
+    constexpr int RPW = kWave / G;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int sub = lane / G;
+    const int sl = lane % G;
+    const int64_t idx = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * RPW + sub;
+    if (idx >= num_rows) return;  // whole lane groups leave together
+    const int row = row_list ? row_list[idx] : static_cast<int>(idx);
+    const int q0 = blockIdx.y * (G * V);
+    int q[V];
+#pragma unroll
+    for (int s = 0; s < V; ++s) {
+        const int qq = q0 + sl + s * G;
+        q[s] = qq < np ? qq : -1;
+    }
+    P acc[V];
+#pragma unroll
+    for (int s = 0; s < V; ++s) acc[s] = pzero<P>();
+    accumulate_range<G, V, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc);
+#pragma unroll
+    for (int s = 0; s < V; ++s)
+        if (q[s] >= 0) Cp[(int64_t)row * ldp + q[s]] = acc[s];
+}
+
+// ----------------------------------------------------------------- baseline
+// One wave per row; lane covers columns lane + 64*i (i < 4) of a 256-column tile.
+__global__ __launch_bounds__(kBlock) void csr_baseline_kernel(
+    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
+    const float* __restrict__ vals, const float* __restrict__ B, float* __restrict__ C,
+    int M, int N) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+    if (row >= M) return;
+    const int n0 = blockIdx.y * 256 + lane;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const int p1 = rowptr[row + 1];
+    for (int p = rowptr[row]; p < p1; ++p) {
+        const int c = colind[p];
+        const float v = vals[p];
+        const float* b = B + (int64_t)c * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = n0 + 64 * i;
+            if (n < N) acc[i] = __builtin_fmaf(v, b[n], acc[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 64 * i;
+        if (n < N) C[(int64_t)row * N + n] = acc[i];
+    }
+}
+
+// ---------------------------------------------------------- ZERO_OVERHEAD_CSR
+// Waves [0, num_chunks) take one 256-nnz chunk each; the 64/G lane groups of
+// the wave split the chunk into contiguous parts and are summed in group order
+// through LDS.  Later waves take 64/G rows of the short-row list each.
+template <int G, int V, typename P>
+__global__ __launch_bounds__(kBlock) void zo_fused_kernel(
+    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
+    const float* __restrict__ vals, const P* __restrict__ Bp, P* __restrict__ Cp,
+    const int32_t* __restrict__ chunk_rows, const int32_t* __restrict__ chunk_starts,
+    const int32_t* __restrict__ chunk_slot, int num_chunks, P* __restrict__ partials,
+    const int32_t* __restrict__ short_rows, int64_t num_short, int64_t ldp, int np) {
+    constexpr int RPW = kWave / G;
+    __shared__ P red[kWavesPerBlock][(RPW > 1 ? RPW - 1 : 1) * G * V];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int sub = lane / G;
+    const int sl = lane % G;
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    const int q0 = blockIdx.y * (G * V);
+    int q[V];
+#pragma unroll
+    for (int s = 0; s < V; ++s) {
+        const int qq = q0 + sl + s * G;
+        q[s] = qq < np ? qq : -1;
+    }
+    P acc[V];
+#pragma unroll
+    for (int s = 0; s < V; ++s) acc[s] = pzero<P>();
+
+    if (gw < num_chunks) {
+        const uint32_t tag = static_cast<uint32_t>(chunk_rows[gw]);
+        const int row = static_cast<int>(tag & ~kSoleFlag);
+        const int cs = chunk_starts[gw];
+        const int ce = min(cs + kChunk, rowptr[row + 1]);
+        constexpr int L = kChunk / RPW;
+        const int a = min(cs + sub * L, ce);
+        const int b = min(a + L, ce);
+        accumulate_range<G, V, P>(colind, vals, Bp, ldp, a, b, sl, q, acc);
+        if constexpr (RPW > 1) {
+            if (sub > 0) {
+#pragma unroll
+                for (int s = 0; s < V; ++s) red[wave][((sub - 1) * V + s) * G + sl] = acc[s];
+            }
+            // LDS writes of groups 1.. must land before group 0 reads them
+            // (same wave: a workgroup-scope fence orders the LDS accesses).
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            if (sub == 0) {
+                for (int h = 1; h < RPW; ++h) {
+#pragma unroll
+                    for (int s = 0; s < V; ++s)
+                        acc[s] = padd(acc[s], red[wave][((h - 1) * V + s) * G + sl]);
+                }
+            }
+        }
+        if (sub == 0) {
+            const int slot = chunk_slot[gw];
+            P* dst = (tag & kSoleFlag) ? Cp + (int64_t)row * ldp : partials + (int64_t)slot * ldp;
+#pragma unroll
+            for (int s = 0; s < V; ++s)
+                if (q[s] >= 0) dst[q[s]] = acc[s];
+        }
+        return;
+    }
+    const int64_t idx = (gw - num_chunks) * RPW + sub;
+    if (idx >= num_short) return;
+    const int row = short_rows[idx];
+    accumulate_range<G, V, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc);
+#pragma unroll
+    for (int s = 0; s < V; ++s)
+        if (q[s] >= 0) Cp[(int64_t)row * ldp + q[s]] = acc[s];
+}
+
+// Deterministic merge: C[row] = ((slot0 + slot1) + slot2) + ... per element.
+template <typename P>
+__global__ __launch_bounds__(kBlock) void zo_merge_kernel(
+    const int32_t* __restrict__ split_rows, const int32_t* __restrict__ split_off,
+    const P* __restrict__ partials, P* __restrict__ Cp, int64_t ldp, int np) {
+    const int r = blockIdx.x;
+    const int qq = blockIdx.y * kBlock + threadIdx.x;
+    if (qq >= np) return;
+    const int o0 = split_off[r], o1 = split_off[r + 1];
+    P acc = partials[(int64_t)o0 * ldp + qq];
+    for (int o = o0 + 1; o < o1; ++o) acc = padd(acc, partials[(int64_t)o * ldp + qq]);
+    Cp[(int64_t)split_rows[r] * ldp + qq] = acc;
+}
+
+// ------------------------------------------------------------------ features
+constexpr int kMomentBlocks = 512;
+
+__device__ __forceinline__ long long wave_sum_ll(long long v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Per-block partials: [block][0] = sum d^2, [1] = max d, [2] = empty rows.
+__global__ __launch_bounds__(kBlock) void degree_moments_partial(
+    const int32_t* __restrict__ rowptr, int M, long long* __restrict__ part) {
+    __shared__ long long s_sq[kWavesPerBlock], s_em[kWavesPerBlock];
+    __shared__ int s_mx[kWavesPerBlock];
+    long long sq = 0, em = 0;
+    int mx = 0;
+    for (int r = blockIdx.x * kBlock + threadIdx.x; r < M; r += gridDim.x * kBlock) {
+        const long long d = (long long)rowptr[r + 1] - rowptr[r];
+        sq += d * d;
+        em += (d == 0);
+        mx = max(mx, (int)d);
+    }
+    sq = wave_sum_ll(sq);
+    em = wave_sum_ll(em);
+    mx = wave_max_i(mx);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        s_sq[wave] = sq;
+        s_em[wave] = em;
+        s_mx[wave] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long a = 0, e = 0;
+        int m = 0;
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+            a += s_sq[w];
+            e += s_em[w];
+            m = max(m, s_mx[w]);
+        }
+        part[blockIdx.x * 3 + 0] = a;
+        part[blockIdx.x * 3 + 1] = m;
+        part[blockIdx.x * 3 + 2] = e;
+    }
+}
+
+// Single block: out = {nnz, sum d^2, max d, empty rows}.
+__global__ __launch_bounds__(kBlock) void degree_moments_final(
+    const long long* __restrict__ part, int nparts, const int32_t* __restrict__ rowptr, int M,
+    long long* __restrict__ out) {
+    __shared__ long long s_sq[kWavesPerBlock], s_em[kWavesPerBlock];
+    __shared__ int s_mx[kWavesPerBlock];
+    long long sq = 0, em = 0;
+    int mx = 0;
+    for (int i = threadIdx.x; i < nparts; i += kBlock) {
+        sq += part[i * 3 + 0];
+        mx = max(mx, (int)part[i * 3 + 1]);
+        em += part[i * 3 + 2];
+    }
+    sq = wave_sum_ll(sq);
+    em = wave_sum_ll(em);
+    mx = wave_max_i(mx);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        s_sq[wave] = sq;
+        s_em[wave] = em;
+        s_mx[wave] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long a = 0, e = 0;
+        int m = 0;
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+            a += s_sq[w];
+            e += s_em[w];
+            m = max(m, s_mx[w]);
+        }
+        out[0] = (long long)rowptr[M] - rowptr[0];
+        out[1] = a;
+        out[2] = m;
+        out[3] = e;
+    }
+}
+
+// Per-device reduction buffers, allocated once and kept for the process.
+struct MomentBuffers {
+    long long* part = nullptr;
+    long long* result = nullptr;
+    long long* host = nullptr;  // pinned
+};
+std::mutex g_moment_mutex;
+MomentBuffers g_moment[64];
+
+// --------------------------------------------------------------- dispatch
+struct LaneShape {
+    int G, V;
+};
+
+// Lane-group shape from the number of packets per row.
+LaneShape pick_shape(int np) {
+    if (np <= 4) return {4, 1};
+    if (np <= 8) return {8, 1};
+    if (np <= 16) return {16, 1};
+    if (np <= 32) return {32, 1};
+    if (np <= 64) return {64, 1};
+    if (np <= 128) return {64, 2};
+    return {64, 4};
+}
+
+template <typename P>
+ra_status launch_csr_rows(int G, int V, dim3 grid, hipStream_t st, const int32_t* rowptr,
+                          const int32_t* colind, const float* vals, const P* B, P* C,
+                          const int32_t* row_list, int64_t num_rows, int64_t ldp, int np) {
+#define RA_ROWS_CASE(g, v)                                                                  \
+    if (G == g && V == v) {                                                                 \
+        csr_rows_kernel<g, v, P><<<grid, kBlock, 0, st>>>(rowptr, colind, vals, B, C,       \
+                                                          row_list, num_rows, ldp, np);     \
+        RA_LAUNCH_CHECK("csr_rows_kernel");                                                 \
+        return RA_OK;                                                                       \
+    }
+    RA_ROWS_CASE(4, 1)
+    RA_ROWS_CASE(8, 1)
+    RA_ROWS_CASE(16, 1)
+    RA_ROWS_CASE(32, 1)
+    RA_ROWS_CASE(64, 1)
+    RA_ROWS_CASE(64, 2)
+    RA_ROWS_CASE(64, 4)
+#undef RA_ROWS_CASE
+    return ra::fail(RA_ERR_INTERNAL, "csr_rows: no lane shape");
+}
+
+template <typename P>
+ra_status launch_zo(int G, int V, dim3 grid, hipStream_t st, const int32_t* rowptr,
+                    const int32_t* colind, const float* vals, const P* B, P* C,
+                    const int32_t* chunk_rows, const int32_t* chunk_starts,
+                    const int32_t* chunk_slot, int num_chunks, P* partials,
+                    const int32_t* short_rows, int64_t num_short, int64_t ldp, int np) {
+#define RA_ZO_CASE(g, v)                                                                     \
+    if (G == g && V == v) {                                                                  \
+        zo_fused_kernel<g, v, P><<<grid, kBlock, 0, st>>>(                                   \
+            rowptr, colind, vals, B, C, chunk_rows, chunk_starts, chunk_slot, num_chunks,    \
+            partials, short_rows, num_short, ldp, np);                                       \
+        RA_LAUNCH_CHECK("zo_fused_kernel");                                                  \
+        return RA_OK;                                                                        \
+    }
+    RA_ZO_CASE(4, 1)
+    RA_ZO_CASE(8, 1)
+    RA_ZO_CASE(16, 1)
+    RA_ZO_CASE(32, 1)
+    RA_ZO_CASE(64, 1)
+    RA_ZO_CASE(64, 2)
+    RA_ZO_CASE(64, 4)
+#undef RA_ZO_CASE
+    return ra::fail(RA_ERR_INTERNAL, "zo: no lane shape");
+}
+
+ra_status check_spmm_args(const void* rowptr, const void* colind, const void* vals,
+                          const void* B, const void* C, int32_t M, int32_t K, int32_t N,
+                          int64_t nnz) {
+    if (M < 0 || K < 0 || N < 0 || nnz < 0)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "negative dimension");
+    if (M > 0 && !rowptr) return ra::fail(RA_ERR_INVALID_ARGUMENT, "rowptr is NULL");
+    if (nnz > 0 && (!colind || !vals)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "colind/vals NULL");
+    if (M > 0 && N > 0 && !C) return ra::fail(RA_ERR_INVALID_ARGUMENT, "C is NULL");
+    if (nnz > 0 && N > 0 && !B) return ra::fail(RA_ERR_INVALID_ARGUMENT, "B is NULL");
+    if (nnz > INT32_MAX) return ra::fail(RA_ERR_UNSUPPORTED, "nnz exceeds int32 indexing");
+    return RA_OK;
+}
+
+}  // namespace
+
+// ============================================================ ZO plan object
+struct ra_zo_plan {
+    ra_zo_info info{};
+    int device = 0;
+    ra::DeviceBuffer chunk_rows, chunk_starts, chunk_slot, short_rows, split_rows, split_off;
+    ra::DeviceBuffer partials;  // grown per N, reused across runs
+    int64_t num_short_total = 0; // empty + tiny + short + medium
+};
+
+extern "C" {
+
+ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
+                             const float* d_vals, const float* d_B, float* d_C, int32_t M,
+                             int32_t K, int32_t N, int64_t nnz, ra_stream_t stream) {
+    RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals, d_B, d_C, M, K, N, nnz));
+    if (M == 0 || N == 0) return RA_OK;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
+    const int np = vec ? N / 4 : N;
+    const LaneShape sh = pick_shape(np);
+    const int rows_per_block = kWavesPerBlock * (kWave / sh.G);
+    dim3 grid((M + rows_per_block - 1) / rows_per_block, (np + sh.G * sh.V - 1) / (sh.G * sh.V));
+    if (vec)
+        return launch_csr_rows<float4>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals,
+                                       reinterpret_cast<const float4*>(d_B),
+                                       reinterpret_cast<float4*>(d_C), nullptr, M, np, np);
+    return launch_csr_rows<float>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
+                                  nullptr, M, np, np);
+}
+
+ra_status ra_spmm_csr_baseline(const int32_t* d_rowptr, const int32_t* d_colind,
+                               const float* d_vals, const float* d_B, float* d_C, int32_t M,
+                               int32_t K, int32_t N, int64_t nnz, ra_stream_t stream) {
+    RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals, d_B, d_C, M, K, N, nnz));
+    if (M == 0 || N == 0) return RA_OK;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    dim3 grid((M + kWavesPerBlock - 1) / kWavesPerBlock, (N + 255) / 256);
+    csr_baseline_kernel<<<grid, kBlock, 0, st>>>(d_rowptr, d_colind, d_vals, d_B, d_C, M, N);
+    RA_LAUNCH_CHECK("csr_baseline_kernel");
+    return RA_OK;
+}
+
+// --------------------------------------------------------------- features
+ra_status ra_features_device(const int32_t* d_rowptr, int32_t M, int32_t K, int32_t N,
+                             ra_stream_t stream, ra_features* out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: out is NULL");
+    if (M < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: M < 0");
+    if (M == 0) return ra_features_from_moments(0, K, N, 0, 0, 0, 0, out);
+    if (!d_rowptr) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: rowptr is NULL");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    int dev = 0;
+    RA_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return ra::fail(RA_ERR_UNSUPPORTED, "features: device id >= 64");
+    MomentBuffers* mb = &g_moment[dev];
+    {
+        std::lock_guard<std::mutex> lock(g_moment_mutex);
+        if (!mb->part) {
+            RA_HIP_TRY(hipMalloc(&mb->part, sizeof(long long) * 3 * kMomentBlocks));
+            RA_HIP_TRY(hipMalloc(&mb->result, sizeof(long long) * 4));
+            RA_HIP_TRY(hipHostMalloc(&mb->host, sizeof(long long) * 4, hipHostMallocDefault));
+        }
+    }
+    const int blocks = std::max(1, std::min(kMomentBlocks, (M + kBlock * 4 - 1) / (kBlock * 4)));
+    degree_moments_partial<<<blocks, kBlock, 0, st>>>(d_rowptr, M, mb->part);
+    RA_LAUNCH_CHECK("degree_moments_partial");
+    degree_moments_final<<<1, kBlock, 0, st>>>(mb->part, blocks, d_rowptr, M, mb->result);
+    RA_LAUNCH_CHECK("degree_moments_final");
+    RA_HIP_TRY(hipMemcpyAsync(mb->host, mb->result, sizeof(long long) * 4, hipMemcpyDeviceToHost, st));
+    RA_HIP_TRY(hipStreamSynchronize(st));
+    return ra_features_from_moments(M, K, N, mb->host[0], mb->host[1],
+                                    static_cast<int32_t>(mb->host[2]), mb->host[3], out);
+}
+
+// --------------------------------------------------------------------- ZO
+ra_status ra_zo_bins_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_t* small_rows,
+                          int32_t* chunk_rows, int32_t* chunk_starts, int32_t* empty_rows,
+                          ra_zo_info* info) {
+    // Binning of csr/ra_zero_overhead.cu:331-358 (same thresholds and chunk
+    // layout); the small list is tiny, short, medium, each ascending.
+    if (!info) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: info is NULL");
+    if (M < 0 || (M > 0 && !h_rowptr)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: bad rowptr");
+    ra_zo_info z{};
+    z.M = M;
+    z.K = K;
+    int64_t max_long = 0;
+    for (int32_t i = 0; i < M; ++i) {
+        const int64_t d = (int64_t)h_rowptr[i + 1] - h_rowptr[i];
+        if (d < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: rowptr not monotone");
+        if (d == 0) ++z.num_empty;
+        else if (d <= kTiny) ++z.num_tiny;
+        else if (d <= kShort) ++z.num_short;
+        else if (d <= kMedium) ++z.num_medium;
+        else {
+            ++z.num_long;
+            max_long = std::max(max_long, d);
+            const int nch = static_cast<int>((d + kChunk - 1) / kChunk);
+            z.num_chunks += nch;
+            if (nch == 1) ++z.num_sole_chunks;
+            else {
+                ++z.num_split_rows;
+                z.num_split_chunks += nch;
+            }
+        }
+    }
+    z.num_small = z.num_tiny + z.num_short + z.num_medium;
+    z.max_long_chunks = static_cast<int32_t>((max_long + kChunk - 1) / kChunk);
+    int64_t t = 0, s = z.num_tiny, m = (int64_t)z.num_tiny + z.num_short, c = 0, e = 0;
+    for (int32_t i = 0; i < M; ++i) {
+        const int32_t start = h_rowptr[i];
+        const int64_t d = (int64_t)h_rowptr[i + 1] - start;
+        if (d == 0) {
+            if (empty_rows) empty_rows[e] = i;
+            ++e;
+        } else if (d <= kTiny) {
+            if (small_rows) small_rows[t] = i;
+            ++t;
+        } else if (d <= kShort) {
+            if (small_rows) small_rows[s] = i;
+            ++s;
+        } else if (d <= kMedium) {
+            if (small_rows) small_rows[m] = i;
+            ++m;
+        } else {
+            const bool sole = d <= kChunk;
+            for (int64_t off = 0; off < d; off += kChunk) {
+                if (chunk_rows) chunk_rows[c] = sole ? static_cast<int32_t>(uint32_t(i) | kSoleFlag) : i;
+                if (chunk_starts) chunk_starts[c] = static_cast<int32_t>(start + off);
+                ++c;
+            }
+        }
+    }
+    z.plan_bytes = (int64_t)sizeof(int32_t) *
+                   ((int64_t)z.num_small + z.num_empty + 3LL * z.num_chunks + 2LL * z.num_split_rows + 1);
+    *info = z;
+    return RA_OK;
+}
+
+ra_status ra_zo_plan_create(const int32_t* h_rowptr, int32_t M, int32_t K, ra_zo_plan** out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: out is NULL");
+    *out = nullptr;
+    ra_zo_info z{};
+    RA_TRY(ra_zo_bins_host(h_rowptr, M, K, nullptr, nullptr, nullptr, nullptr, &z));
+    std::vector<int32_t> small(z.num_small), empty(z.num_empty), crow(z.num_chunks),
+        cstart(z.num_chunks);
+    RA_TRY(ra_zo_bins_host(h_rowptr, M, K, small.data(), crow.data(), cstart.data(), empty.data(), &z));
+    // Short-row list handed to the kernel: empty rows first (they only write
+    // zeros), then the bin-ordered small rows.
+    std::vector<int32_t> short_rows;
+    short_rows.reserve(empty.size() + small.size());
+    short_rows.insert(short_rows.end(), empty.begin(), empty.end());
+    short_rows.insert(short_rows.end(), small.begin(), small.end());
+    // Partial slots of split rows: consecutive and ascending per row.
+    std::vector<int32_t> slot(z.num_chunks, -1), split_rows, split_off{0};
+    int32_t next = 0;
+    for (int32_t c = 0; c < z.num_chunks;) {
+        const uint32_t tag = static_cast<uint32_t>(crow[c]);
+        if (tag & kSoleFlag) {
+            ++c;
+            continue;
+        }
+        const int32_t row = crow[c];
+        split_rows.push_back(row);
+        while (c < z.num_chunks && crow[c] == row) slot[c++] = next++;
+        split_off.push_back(next);
+    }
+    auto plan = new (std::nothrow) ra_zo_plan();
+    if (!plan) return ra::fail(RA_ERR_OUT_OF_MEMORY, "zo: plan allocation");
+    ra_status s = RA_OK;
+    (void)hipGetDevice(&plan->device);
+    if ((s = plan->chunk_rows.upload(crow)) == RA_OK && (s = plan->chunk_starts.upload(cstart)) == RA_OK &&
+        (s = plan->chunk_slot.upload(slot)) == RA_OK && (s = plan->short_rows.upload(short_rows)) == RA_OK &&
+        (s = plan->split_rows.upload(split_rows)) == RA_OK && (s = plan->split_off.upload(split_off)) == RA_OK) {
+        plan->info = z;
+        plan->num_short_total = static_cast<int64_t>(short_rows.size());
+        *out = plan;
+        return RA_OK;
+    }
+    delete plan;
+    return s;
+}
+
+ra_status ra_zo_plan_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
+                         const float* d_vals, const float* d_B, float* d_C, int32_t N,
+                         ra_stream_t stream) {
+    return ra_zo_plan_run_stage(plan, d_rowptr, d_colind, d_vals, d_B, d_C, N, 0, stream);
+}
+
+ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
+                               const int32_t* d_colind, const float* d_vals, const float* d_B,
+                               float* d_C, int32_t N, int32_t stage, ra_stream_t stream) {
+    if (stage < 0 || stage > 2) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: stage must be 0, 1 or 2");
+    if (!plan) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: plan is NULL");
+    const int32_t M = plan->info.M;
+    RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals, d_B, d_C, M, plan->info.K, N, 0));
+    if (M == 0 || N == 0) return RA_OK;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
+    const int np = vec ? N / 4 : N;
+    const LaneShape sh = pick_shape(np);
+    if (plan->info.num_split_chunks > 0)
+        RA_TRY(plan->partials.ensure((size_t)plan->info.num_split_chunks * N * sizeof(float)));
+    const int RPW = kWave / sh.G;
+    const int64_t waves = plan->info.num_chunks + (plan->num_short_total + RPW - 1) / RPW;
+    const int tiles = (np + sh.G * sh.V - 1) / (sh.G * sh.V);
+    if (waves > 0 && stage != 2) {
+        dim3 grid((waves + kWavesPerBlock - 1) / kWavesPerBlock, tiles);
+        ra_status s;
+        if (vec)
+            s = launch_zo<float4>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals,
+                                  reinterpret_cast<const float4*>(d_B), reinterpret_cast<float4*>(d_C),
+                                  plan->chunk_rows.get<int32_t>(), plan->chunk_starts.get<int32_t>(),
+                                  plan->chunk_slot.get<int32_t>(), plan->info.num_chunks,
+                                  plan->partials.get<float4>(), plan->short_rows.get<int32_t>(),
+                                  plan->num_short_total, np, np);
+        else
+            s = launch_zo<float>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
+                                 plan->chunk_rows.get<int32_t>(), plan->chunk_starts.get<int32_t>(),
+                                 plan->chunk_slot.get<int32_t>(), plan->info.num_chunks,
+                                 plan->partials.get<float>(), plan->short_rows.get<int32_t>(),
+                                 plan->num_short_total, np, np);
+        RA_TRY(s);
+    }
+    if (plan->info.num_split_rows > 0 && stage != 1) {
+        dim3 grid(plan->info.num_split_rows, (np + kBlock - 1) / kBlock);
+        if (vec)
+            zo_merge_kernel<float4><<<grid, kBlock, 0, st>>>(
+                plan->split_rows.get<int32_t>(), plan->split_off.get<int32_t>(),
+                plan->partials.get<float4>(), reinterpret_cast<float4*>(d_C), np, np);
+        else
+            zo_merge_kernel<float><<<grid, kBlock, 0, st>>>(
+                plan->split_rows.get<int32_t>(), plan->split_off.get<int32_t>(),
+                plan->partials.get<float>(), d_C, np, np);
+        RA_LAUNCH_CHECK("zo_merge_kernel");
+    }
+    return RA_OK;
+}
+
+ra_status ra_zo_plan_get_info(const ra_zo_plan* plan, ra_zo_info* info) {
+    if (!plan || !info) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: NULL argument");
+    *info = plan->info;
+    return RA_OK;
+}
+
+void ra_zo_plan_destroy(ra_zo_plan* plan) { delete plan; }
+
+}  // extern "C"

@@ -1,0 +1,300 @@
+// router.cpp — routing features (shared finalisation) and the seven-rule router.
+//
+// Compiled with -ffp-contract=off: every floating-point step below must be the
+// same IEEE operation sequence as the Python mirror (ra_spmm/router.py), so
+// the two make bit-identical decisions.
+//
+// Reference: compute_production_router_features, router/router_features.cpp:79-111;
+//            compute_production_router_features_gpu, router/router_features_cuda.cu:51-92;
+//            route_dispatch deployed block, router/router_dispatch.cpp:979-1110;
+//            compute_feasible, router/router_dispatch.cpp:107-464.
+#include <cmath>
+#include <cstring>
+
+#include "ra_internal.hpp"
+
+namespace {
+
+// Threshold table of the rule tree.  Field names follow the rule they gate.
+struct RouterTable {
+    float cv_extreme;        // rule 1: cv >= -> ZERO_OVERHEAD_CSR
+    float cv_uniform;        // rule 2: cv <
+    float d_ultralow;        //   d <
+    int   n_ultralow_csr;    //   N <= -> CSR_DIRECT
+    float cv_comm_lo;        //   cv >=
+    float d_comm;            //   d <
+    int   n_comm_csr;        //   N <= -> CSR_DIRECT
+    float cv_skewed;         // rule 3: cv >=
+    int   m_skewed_large;    //   M >= -> COMMUNITY_TC else SEGMENT_HYBRID
+    float d_dense;           // rule 4: d >=
+    int   m_small;           // rule 5: M <
+    float d_small_dense;     //   d >=
+    int   n_small_narrow;    //   N < -> CUSPARSE (baseline CSR)
+    int   n_small_mid;       //   N < -> SEGMENT_HYBRID
+    float d_heavy;           // rule 6: d >=
+    float cv_heavy;          //   cv >=
+    float d_web;             // rule 7: d <
+    float cv_web_lo;         //   cv in [lo, hi]
+    float cv_web_hi;
+    int   m_web;             //   M >=
+    float cv_gate_csr;       // tile gated: cv < -> CSR_DIRECT else ZERO_OVERHEAD_CSR
+    double plan_s_per_nnz;   // tile gate: est build seconds per nnz (d*M)
+    double plan_budget_s;    //   withheld above this
+    float d_fp32_route;      // precision: d < -> FP32 route
+    int   m_fp32_small;      //   or (M <= and
+    float d_fp32_small;      //       d <)
+    // MI355X-only knobs (inert in the reference table).
+    int   fp32_route_csr;    // FP32-route picks go to the CSR family instead
+    int   skewed_to_zo;      // rule 3 sends skewed graphs to ZERO_OVERHEAD_CSR
+    float zo_min_cv;         // CSR_DIRECT picks with cv >= this go to ZERO_OVERHEAD_CSR
+};
+
+// Published thresholds (router/router_dispatch.cpp:1004-1094, ra_router_eval.py:37-124).
+constexpr RouterTable kReference = {
+    5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
+    25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 2e-8, 20.0, 5.0f, 25000, 9.0f,
+    0, 0, 1e30f};
+
+// MI355X calibration.  Structure of the tree is unchanged; the knobs below are
+// set from the gfx950 sweep (bench.py --calibrate):
+//  - tile gate: host ME-BCRS build plus upload cost per nnz on the MI355X host;
+//  - skewed graphs (cv >= 3) -> hub-chunked ZERO_OVERHEAD_CSR;
+//  - FP32-route tile picks -> the CSR family (the FP32 route reads B in fp32
+//    and pays block padding on wave64);
+//  - CSR_DIRECT picks on skewed rows (cv >= 1.5) -> ZERO_OVERHEAD_CSR.
+constexpr RouterTable kMI355X = {
+    5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
+    25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-8, 20.0, 5.0f, 25000, 9.0f,
+    1, 1, 1.5f};
+
+bool tile_family(int p) {
+    return p == RA_PATH_TC_DIRECT || p == RA_PATH_COMMUNITY_TC || p == RA_PATH_SEGMENT_HYBRID;
+}
+
+bool in_main_portfolio(int p) {
+    // router/router_dispatch.cpp:50-72
+    switch (p) {
+        case RA_PATH_CSR_DIRECT: case RA_PATH_ROW_SPLIT_CUDA: case RA_PATH_TC_REORDERED:
+        case RA_PATH_HYBRID_TC_CUDA: case RA_PATH_CUSPARSE: case RA_PATH_RODE_ENHANCED:
+        case RA_PATH_VECTORIZED_COARSE: case RA_PATH_LOCALITY_TILED: case RA_PATH_TC_DIRECT:
+        case RA_PATH_COMMUNITY_TC: case RA_PATH_ZERO_OVERHEAD_CSR: case RA_PATH_SEGMENT_HYBRID:
+            return true;
+        default:
+            return false;
+    }
+}
+
+// Kernels this engine implements.  Legacy/ablation paths of the reference are
+// reported infeasible (they are not built on MI355X).
+bool implemented(int p) {
+    return p == RA_PATH_CSR_DIRECT || p == RA_PATH_CUSPARSE || p == RA_PATH_TC_DIRECT ||
+           p == RA_PATH_COMMUNITY_TC || p == RA_PATH_ZERO_OVERHEAD_CSR ||
+           p == RA_PATH_SEGMENT_HYBRID;
+}
+
+}  // namespace
+
+extern "C" {
+
+ra_status ra_features_from_moments(int32_t M, int32_t K, int32_t N, int64_t nnz,
+                                   int64_t sum_deg_sq, int32_t max_deg, int64_t empty_rows,
+                                   ra_features* out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: out is NULL");
+    std::memset(out, 0, sizeof(*out));
+    out->M = M;
+    out->K = K;
+    out->N = N;
+    out->nnz = nnz;
+    out->sum_deg_sq = sum_deg_sq;
+    out->max_deg = max_deg;
+    out->empty_rows = empty_rows;
+    if (M <= 0) return RA_OK;
+    // Moment form of router/router_features_cuda.cu:83-91 on exact integers.
+    const double avg = static_cast<double>(nnz) / static_cast<double>(M);
+    double var = static_cast<double>(sum_deg_sq) / static_cast<double>(M) - avg * avg;
+    if (var < 0.0) var = 0.0;
+    const double std_dev = std::sqrt(var);
+    out->avg = avg;
+    out->std_dev = std_dev;
+    out->avg_nnz_per_row = static_cast<float>(avg);
+    out->std_nnz_per_row = static_cast<float>(std_dev);
+    out->degree_cv = (avg > 1e-6) ? static_cast<float>(std_dev / avg) : 0.0f;
+    out->max_to_mean_ratio = (avg > 1e-6) ? static_cast<float>(max_deg / avg) : 0.0f;
+    return RA_OK;
+}
+
+ra_status ra_features_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_t N,
+                           ra_features* out) {
+    if (!h_rowptr && M > 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: rowptr is NULL");
+    if (M < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: M < 0");
+    int64_t s2 = 0, empty = 0;
+    int32_t mx = 0;
+    for (int32_t r = 0; r < M; ++r) {
+        const int64_t d = static_cast<int64_t>(h_rowptr[r + 1]) - h_rowptr[r];
+        if (d < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: rowptr not monotone");
+        s2 += d * d;
+        if (d > mx) mx = static_cast<int32_t>(d);
+        empty += (d == 0);
+    }
+    const int64_t nnz = M > 0 ? static_cast<int64_t>(h_rowptr[M]) - h_rowptr[0] : 0;
+    return ra_features_from_moments(M, K, N, nnz, s2, mx, empty, out);
+}
+
+ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t table,
+                            ra_route* out) {
+    if (!f || !out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "route: NULL argument");
+    if (table != RA_TABLE_REFERENCE && table != RA_TABLE_MI355X)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "route: unknown threshold table");
+    const RouterTable& T = (table == RA_TABLE_REFERENCE) ? kReference : kMI355X;
+    std::memset(out, 0, sizeof(*out));
+
+    const float d = f->avg_nnz_per_row;
+    const float cv = f->degree_cv;
+    const int N = f->N;
+    const int M = f->M;
+
+    // Feasibility (router/router_dispatch.cpp:107-464 restricted to the MAIN
+    // production features): tile families need N >= 16.
+    for (int p = 0; p < RA_PATH_COUNT; ++p) {
+        bool ok = true;
+        int8_t code = RA_REJECT_CHOSEN;
+        if (portfolio == RA_PORTFOLIO_MAIN && !in_main_portfolio(p)) {
+            ok = false;
+            code = RA_REJECT_NOT_IN_PORTFOLIO;
+        } else if (!implemented(p)) {
+            ok = false;
+            code = RA_REJECT_NOT_FEASIBLE;
+        } else if (tile_family(p) && N < 16) {
+            ok = false;
+            code = RA_REJECT_MARGIN_TOO_SMALL;
+        }
+        out->feasible[p] = ok ? 1 : 0;
+        out->rejection_code[p] = code;
+    }
+
+    int choice = out->feasible[RA_PATH_TC_DIRECT] ? RA_PATH_TC_DIRECT : RA_PATH_CSR_DIRECT;
+    const char* reason = out->feasible[RA_PATH_TC_DIRECT] ? "tc_direct_default_winner"
+                                                           : "csr_direct_tc_direct_infeasible";
+    float risk = 0.05f;
+    bool fp32_route = false;
+    int rule = 0;
+
+    // Preprocessing-aware tile gate (router/router_dispatch.cpp:1006-1013).
+    const double est_plan_s = T.plan_s_per_nnz * static_cast<double>(d) * static_cast<double>(M);
+    const bool tile_ok = out->feasible[RA_PATH_TC_DIRECT] && est_plan_s <= T.plan_budget_s;
+
+    auto csr_by_skew = [&](const char* csr_reason, const char* zo_reason) {
+        if (cv < T.cv_gate_csr) {
+            choice = RA_PATH_CSR_DIRECT;
+            reason = csr_reason;
+            risk = 0.05f;
+        } else {
+            choice = RA_PATH_ZERO_OVERHEAD_CSR;
+            reason = zo_reason;
+            risk = 0.06f;
+        }
+    };
+    auto pick_tile = [&](int p, const char* why, bool force_fp32) {
+        if (tile_ok && out->feasible[p]) {
+            const bool want_fp32 =
+                force_fp32 || (d < T.d_fp32_route || (M <= T.m_fp32_small && d < T.d_fp32_small));
+            if (want_fp32 && T.fp32_route_csr) {
+                csr_by_skew("csr_direct_over_fp32_tile", "zero_overhead_over_fp32_tile");
+                return;
+            }
+            choice = p;
+            reason = why;
+            risk = 0.06f;
+            fp32_route = want_fp32;
+        } else {
+            csr_by_skew("csr_direct_tile_gated", "zero_overhead_tile_gated");
+        }
+    };
+
+    if (cv >= T.cv_extreme) {
+        rule = 1;
+        choice = RA_PATH_ZERO_OVERHEAD_CSR;
+        reason = "zero_overhead_extreme_skew";
+        risk = 0.06f;
+    } else if (cv < T.cv_uniform) {
+        rule = 2;
+        if (d < T.d_ultralow) {
+            if (N <= T.n_ultralow_csr) {
+                choice = RA_PATH_CSR_DIRECT;
+                reason = "csr_direct_uniform_ultralow_d";
+                risk = 0.05f;
+            } else {
+                pick_tile(RA_PATH_TC_DIRECT, "tc_direct_uniform_wideN", false);
+            }
+        } else if (cv >= T.cv_comm_lo && d < T.d_comm) {
+            if (N <= T.n_comm_csr) {
+                choice = RA_PATH_CSR_DIRECT;
+                reason = "csr_direct_synth_community";
+                risk = 0.05f;
+            } else {
+                pick_tile(RA_PATH_TC_DIRECT, "tc_direct_community_wideN", true);
+            }
+        } else {
+            pick_tile(RA_PATH_TC_DIRECT, "tc_direct_uniform", false);
+        }
+    } else if (cv >= T.cv_skewed) {
+        rule = 3;
+        if (T.skewed_to_zo) {
+            choice = RA_PATH_ZERO_OVERHEAD_CSR;
+            reason = "zero_overhead_skewed";
+            risk = 0.06f;
+        } else if (M >= T.m_skewed_large) {
+            pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_skewed_large", false);
+        } else {
+            pick_tile(RA_PATH_SEGMENT_HYBRID, "segment_hybrid_skewed_medium", false);
+        }
+    } else if (d >= T.d_dense) {
+        rule = 4;
+        pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_dense_rows", false);
+    } else if (M < T.m_small && d >= T.d_small_dense) {
+        rule = 5;
+        if (N < T.n_small_narrow) {
+            choice = RA_PATH_CUSPARSE;
+            reason = "cusparse_small_dense_narrowN";
+            risk = 0.05f;
+        } else if (N < T.n_small_mid) {
+            pick_tile(RA_PATH_SEGMENT_HYBRID, "segment_hybrid_small_dense", false);
+        } else {
+            pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_small_dense_wideN", false);
+        }
+    } else if (d >= T.d_heavy && cv >= T.cv_heavy) {
+        rule = 6;
+        pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_heavy_mixed", false);
+    } else if (d < T.d_web && cv >= T.cv_web_lo && cv <= T.cv_web_hi && M >= T.m_web) {
+        rule = 7;
+        pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_web_locality", true);
+    } else {
+        rule = 8;
+        pick_tile(RA_PATH_TC_DIRECT, "tc_direct_default", false);
+    }
+
+    // MI355X: a CSR_DIRECT pick on a skewed row distribution serialises hubs
+    // on one lane group; the hub-chunked kernel is the safe CSR choice.
+    if (choice == RA_PATH_CSR_DIRECT && cv >= T.zo_min_cv) {
+        choice = RA_PATH_ZERO_OVERHEAD_CSR;
+        reason = "zero_overhead_skewed_csr";
+        risk = 0.06f;
+    }
+
+    out->chosen_path = choice;
+    out->use_tf32 = (tile_family(choice) && fp32_route) ? 1 : 0;
+    out->rule = rule;
+    out->tile_ok = tile_ok ? 1 : 0;
+    out->estimated_risk = risk;
+    out->est_plan_s = est_plan_s;
+    std::strncpy(out->decision_reason, reason, sizeof(out->decision_reason) - 1);
+    // Every other feasible path lost to the chosen one
+    // (router/router_dispatch.cpp:960-966 / mark_choice :482-499).
+    for (int p = 0; p < RA_PATH_COUNT; ++p) {
+        if (out->feasible[p] && p != choice) out->rejection_code[p] = RA_REJECT_NOT_STRONG_ENOUGH;
+    }
+    out->rejection_code[choice] = RA_REJECT_CHOSEN;
+    return RA_OK;
+}
+
+}  // extern "C"

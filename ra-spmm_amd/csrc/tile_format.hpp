@@ -1,0 +1,47 @@
+// tile_format.hpp — host-side tile format shared by TC_DIRECT, COMMUNITY_TC
+// and SEGMENT_HYBRID.
+//
+// Layout (all arrays flat, row-major):
+//   win_rows[W*8]        output row of window slot (COMMUNITY_TC order; -1 pad)
+//   block_offsets[W+1]   blocks of window w are [block_offsets[w], block_offsets[w+1])
+//   atox[blocks*8]       B row (column of A) gathered by each 8x1 vector; -1 = padding
+//   vals[blocks*64]      block values, [block][window slot r][vector k], fp16 or
+//                        bf16 bits.  One 16-byte row per slot is exactly the
+//                        8-element K-run an MFMA 16x16x32 lane consumes.
+//   SEGMENT_HYBRID only: seg_window/seg_bbegin/seg_bend/seg_slot per segment
+//   (bit 31 of seg_window marks a sole segment, seg_slot = -1), and
+//   split_windows/split_offsets for the deterministic merge.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "../../include/ra_spmm.h"
+
+struct ra_tile_host {
+    int32_t kind = 0, M = 0, K = 0, N = 0, value_dtype = RA_DTYPE_F16;
+    bool active = false;
+    int64_t nnz = 0;          // stored entries after duplicate merge
+    int64_t num_vectors = 0;  // distinct (window, column) pairs
+    int32_t max_window_blocks = 0;
+    std::vector<int32_t> win_rows, block_offsets, atox;
+    std::vector<uint16_t> vals;
+    std::vector<int32_t> seg_window, seg_bbegin, seg_bend, seg_slot, split_windows, split_offsets;
+    double build_ms = 0.0;
+};
+
+namespace ra {
+
+constexpr int kTileWindow = 8;        // rows per window
+constexpr int kTileVec = 8;           // vectors per block
+constexpr int kTileSegBlocks = 64;    // SEGMENT_HYBRID: max blocks per segment
+constexpr uint32_t kTileSoleFlag = 0x80000000u;
+
+uint16_t f32_to_f16_rne(float f);
+uint16_t f32_to_bf16_rne(float f);
+
+ra_status tile_host_build(int32_t kind, const int32_t* rowptr, const int32_t* colind,
+                          const float* vals, int32_t M, int32_t K, int32_t N, int32_t value_dtype,
+                          ra_tile_host& out);
+
+}  // namespace ra

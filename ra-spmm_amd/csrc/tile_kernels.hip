@@ -1,0 +1,510 @@
+// tile_kernels.hip — TC_DIRECT / COMMUNITY_TC / SEGMENT_HYBRID on gfx950.
+//
+// Work item = one window (TC_DIRECT, COMMUNITY_TC) or one segment
+// (SEGMENT_HYBRID): 8 output rows and a run of blocks [b0, b1).
+//
+// FP16/BF16 route (tile_mfma_kernel): one wavefront per (item, 16*CPL-column
+// slice), v_mfma_f32_16x16x32_{f16,bf16}.  A step consumes 4 blocks (32
+// vectors = the MFMA K).  Lane (j = lane & 15, q = lane >> 4):
+//   - gathers B rows atox[(b+q)*8 + v], v < 8, CPL contiguous elements each at
+//     columns col0 + j*CPL (one 16-byte load per vector for CPL = 8), then
+//     transposes in registers so MFMA number cc sees K = vectors, N = column
+//     col0 + j*CPL + cc;
+//   - feeds block b+q as the A fragment in block-diagonal form: rows 0-7 of the
+//     16-row MFMA carry blocks b, b+1 and rows 8-15 carry b+2, b+3, so an 8-row
+//     window fills the 16x16x32 shape; the two halves are summed at the end.
+// FP32 route (tile_fp32_kernel): replaces the reference's TF32 path (gfx950 has
+// no xf32 MFMA): one wavefront per (item, column slice), B read in fp32, exact
+// fp32 FMA of the stored fp16/bf16 value times B, vectors in ascending column
+// order.
+//
+// Reference: fs_tile_spmm[_staged]_kernel tc/ra_tc_direct.cu:109-179, 270-328;
+//            ct_fs_tile_spmm_perm_kernel tc/ra_community_tc.cu:106-190;
+//            sh_fs_tile_spmm_seg_kernel / sh_merge_split_kernel
+//            tc/ra_segment_hybrid.cu:90-221; convert_b_to_half_kernel
+//            tc/ra_tc_direct.cu:85-104.
+#include <algorithm>
+#include <chrono>
+
+#include "ra_internal.hpp"
+#include "tile_format.hpp"
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = kWave * kWavesPerBlock;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+template <int CPL> struct HalfRun;  // CPL contiguous 16-bit elements
+template <> struct HalfRun<1> { typedef unsigned short T; };
+template <> struct HalfRun<2> { typedef unsigned short T __attribute__((ext_vector_type(2))); };
+template <> struct HalfRun<4> { typedef unsigned short T __attribute__((ext_vector_type(4))); };
+template <> struct HalfRun<8> { typedef u16x8 T; };
+
+template <int CPL>
+__device__ __forceinline__ unsigned short run_elem(const typename HalfRun<CPL>::T& r, int i) {
+    if constexpr (CPL == 1) return r;
+    else return r[i];
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma32(u16x8 a, u16x8 b, f32x4 c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+struct Items {
+    const int32_t* block_offsets;  // TC_DIRECT / COMMUNITY_TC
+    const int32_t* seg_window;     // SEGMENT_HYBRID
+    const int32_t* seg_bbegin;
+    const int32_t* seg_bend;
+    const int32_t* seg_slot;
+    const int32_t* win_rows;       // COMMUNITY_TC
+};
+
+template <int KIND>
+__device__ __forceinline__ void item_range(const Items& it, int i, int& w, int& b0, int& b1,
+                                           int& slot) {
+    if constexpr (KIND == RA_TILE_SEGMENT_HYBRID) {
+        w = static_cast<int>(static_cast<uint32_t>(it.seg_window[i]) & 0x7FFFFFFFu);
+        b0 = it.seg_bbegin[i];
+        b1 = it.seg_bend[i];
+        slot = it.seg_slot[i];
+    } else {
+        w = i;
+        b0 = it.block_offsets[i];
+        b1 = it.block_offsets[i + 1];
+        slot = -1;
+    }
+}
+
+// Destination of window slot m (0..7): a C row, or a partial-slot row.
+template <int KIND>
+__device__ __forceinline__ float* item_row(const Items& it, float* C, float* scratch, int w,
+                                           int slot, int m, int M, int N) {
+    if (slot >= 0) return scratch + ((int64_t)slot * ra::kTileWindow + m) * N;
+    int row;
+    if constexpr (KIND == RA_TILE_COMMUNITY_TC) row = it.win_rows[w * ra::kTileWindow + m];
+    else row = w * ra::kTileWindow + m;
+    if (row < 0 || row >= M) return nullptr;
+    return C + (int64_t)row * N;
+}
+
+// ------------------------------------------------------------ MFMA route
+template <int CPL, bool BF16, int KIND>
+__global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
+    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
+    const uint16_t* __restrict__ Bh, int ldb, float* __restrict__ C, float* __restrict__ scratch,
+    int M, int N, int num_items) {
+    typedef typename HalfRun<CPL>::T Run;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
+    if (item >= num_items) return;
+    int w, b0, b1, slot;
+    item_range<KIND>(it, item, w, b0, b1, slot);
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int col = blockIdx.y * (16 * CPL) + j * CPL;
+    const bool col_ok = col < ldb;  // ldb % 8 == 0 and CPL | 8: whole run in bounds
+    const bool a_half = (j < 8) == (q < 2);
+
+    f32x4 acc[CPL];
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) acc[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int b = b0; b < b1; b += 4) {
+        const int bq = b + q;
+        const bool bok = bq < b1;
+        int cols[8];
+        if (bok) {
+            const int4 c0 = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8);
+            const int4 c1 = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8 + 4);
+            cols[0] = c0.x; cols[1] = c0.y; cols[2] = c0.z; cols[3] = c0.w;
+            cols[4] = c1.x; cols[5] = c1.y; cols[6] = c1.z; cols[7] = c1.w;
+        } else {
+#pragma unroll
+            for (int v = 0; v < 8; ++v) cols[v] = -1;
+        }
+        u16x8 a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (bok && a_half) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)bq * 64 + (j & 7) * 8);
+        Run raw[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            if (cols[v] >= 0 && col_ok)
+                raw[v] = *reinterpret_cast<const Run*>(Bh + (int64_t)cols[v] * ldb + col);
+            else
+                raw[v] = Run{};
+        }
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) {
+            u16x8 bop;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) bop[v] = run_elem<CPL>(raw[v], cc);
+            acc[cc] = mfma32<BF16>(a, bop, acc[cc]);
+        }
+    }
+
+    // D[m][n]: lane holds rows 4*(lane>>4)+r, column n = lane & 15.  Rows m and
+    // m+8 are partial sums of the same window row (block-diagonal A).
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[cc][r] += __shfl_down(acc[cc][r], 32, kWave);
+    if (lane >= 32) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * (lane >> 4) + r;
+        float* dst = item_row<KIND>(it, C, scratch, w, slot, m, M, N);
+        if (!dst) continue;
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc)
+            if (col + cc < N) dst[col + cc] = acc[cc][r];
+    }
+}
+
+// ------------------------------------------------------------ FP32 route
+__device__ __forceinline__ float stored_to_f32(uint16_t h, bool bf16) {
+    if (bf16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// One wavefront per (item, slice of 64*F columns); lane covers F consecutive
+// columns.  VEC: F-wide vector loads/stores (needs N % F == 0 and alignment).
+template <int F, bool VEC, int KIND>
+__global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
+    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
+    const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch, int M, int N,
+    int num_items) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
+    if (item >= num_items) return;
+    int w, b0, b1, slot;
+    item_range<KIND>(it, item, w, b0, b1, slot);
+    const int col = blockIdx.y * (64 * F) + lane * F;
+    float acc[8][F];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[r][f] = 0.f;
+    const bool bf = bf16vals != 0;
+    for (int b = b0; b < b1; ++b) {
+        for (int v = 0; v < 8; ++v) {
+            const int c = atox[(int64_t)b * 8 + v];
+            if (c < 0) break;  // padding sits at the end of the last block
+            float bv[F];
+            if constexpr (VEC) {
+                if (col < N) {
+                    if constexpr (F == 4) {
+                        const float4 t = *reinterpret_cast<const float4*>(B + (int64_t)c * N + col);
+                        bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+                    } else if constexpr (F == 2) {
+                        const float2 t = *reinterpret_cast<const float2*>(B + (int64_t)c * N + col);
+                        bv[0] = t.x; bv[1] = t.y;
+                    } else {
+                        bv[0] = B[(int64_t)c * N + col];
+                    }
+                } else {
+#pragma unroll
+                    for (int f = 0; f < F; ++f) bv[f] = 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int f = 0; f < F; ++f) bv[f] = (col + f < N) ? B[(int64_t)c * N + col + f] : 0.f;
+            }
+            const uint16_t* vb = vals + (int64_t)b * 64 + v;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const float a = stored_to_f32(vb[r * 8], bf);
+#pragma unroll
+                for (int f = 0; f < F; ++f) acc[r][f] = __builtin_fmaf(a, bv[f], acc[r][f]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        float* dst = item_row<KIND>(it, C, scratch, w, slot, m, M, N);
+        if (!dst) continue;
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            if (col + f < N) dst[col + f] = acc[m][f];
+    }
+}
+
+// ------------------------------------------------ SEGMENT_HYBRID merge
+// C[w*8+m][n] = ((slot0 + slot1) + ...) in ascending slot order
+// (tc/ra_segment_hybrid.cu:198-221).
+__global__ __launch_bounds__(kBlock) void tile_merge_kernel(
+    const int32_t* __restrict__ split_windows, const int32_t* __restrict__ split_offsets,
+    const float* __restrict__ scratch, float* __restrict__ C, int M, int N) {
+    const int sw = blockIdx.x;
+    const int64_t e = (int64_t)blockIdx.y * kBlock + threadIdx.x;
+    if (e >= (int64_t)ra::kTileWindow * N) return;
+    const int m = static_cast<int>(e / N);
+    const int n = static_cast<int>(e - (int64_t)m * N);
+    const int row = split_windows[sw] * ra::kTileWindow + m;
+    if (row >= M) return;
+    const int o0 = split_offsets[sw], o1 = split_offsets[sw + 1];
+    float acc = scratch[((int64_t)o0 * ra::kTileWindow + m) * N + n];
+    for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * ra::kTileWindow + m) * N + n];
+    C[(int64_t)row * N + n] = acc;
+}
+
+// --------------------------------------------------------------- convert
+// fp32 [rows, cols] -> 16-bit [rows, ldo], RNE, columns cols..ldo-1 zeroed.
+// One thread writes 8 consecutive outputs (one 16-byte store).
+template <bool BF16>
+__global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict__ in,
+                                                         uint16_t* __restrict__ out, int64_t rows,
+                                                         int cols, int ldo) {
+    const int groups = ldo / 8;
+    const int64_t total = rows * groups;
+    for (int64_t g = (int64_t)blockIdx.x * kBlock + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * kBlock) {
+        const int64_t r = g / groups;
+        const int c0 = static_cast<int>(g - r * groups) * 8;
+        const float* src = in + r * cols;
+        u16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = (c0 + i < cols) ? src[c0 + i] : 0.f;
+            if constexpr (BF16) o[i] = __builtin_bit_cast(unsigned short, static_cast<__bf16>(x));
+            else o[i] = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x));
+        }
+        *reinterpret_cast<u16x8*>(out + r * ldo + c0) = o;
+    }
+}
+
+ra_status launch_convert(const float* in, void* out, int64_t rows, int32_t cols, int32_t ldo,
+                         bool bf16, hipStream_t st) {
+    if (rows <= 0 || ldo <= 0) return RA_OK;
+    const int64_t total = rows * (ldo / 8);
+    const int blocks = static_cast<int>(std::min<int64_t>((total + kBlock - 1) / kBlock, 1 << 16));
+    if (bf16)
+        convert_kernel<true><<<blocks, kBlock, 0, st>>>(in, static_cast<uint16_t*>(out), rows, cols, ldo);
+    else
+        convert_kernel<false><<<blocks, kBlock, 0, st>>>(in, static_cast<uint16_t*>(out), rows, cols, ldo);
+    RA_LAUNCH_CHECK("convert_kernel");
+    return RA_OK;
+}
+
+}  // namespace
+
+// ============================================================ plan object
+struct ra_tile_plan {
+    ra_tile_info info{};
+    int32_t num_items = 0;
+    ra::DeviceBuffer block_offsets, atox, vals, win_rows, seg_window, seg_bbegin, seg_bend,
+        seg_slot, split_windows, split_offsets;
+    ra::DeviceBuffer bconv;    // B converted to fp16/bf16 (grown per K*ldb)
+    ra::DeviceBuffer scratch;  // SEGMENT_HYBRID partial slots
+};
+
+namespace {
+
+Items plan_items(const ra_tile_plan* p) {
+    Items it{};
+    it.block_offsets = p->block_offsets.get<int32_t>();
+    it.seg_window = p->seg_window.get<int32_t>();
+    it.seg_bbegin = p->seg_bbegin.get<int32_t>();
+    it.seg_bend = p->seg_bend.get<int32_t>();
+    it.seg_slot = p->seg_slot.get<int32_t>();
+    it.win_rows = p->win_rows.get<int32_t>();
+    return it;
+}
+
+template <int KIND>
+ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, bool bf16, float* C,
+                           float* scratch, int N, hipStream_t st) {
+    const int M = p->info.M;
+    const Items it = plan_items(p);
+    const int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
+    dim3 grid((p->num_items + kWavesPerBlock - 1) / kWavesPerBlock, (N + 16 * cpl - 1) / (16 * cpl));
+#define RA_MFMA_CASE(c)                                                                            \
+    if (cpl == c) {                                                                                \
+        if (bf16)                                                                                  \
+            tile_mfma_kernel<c, true, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),    \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items);                 \
+        else                                                                                       \
+            tile_mfma_kernel<c, false, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),   \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items);                 \
+    }
+    RA_MFMA_CASE(1)
+    RA_MFMA_CASE(2)
+    RA_MFMA_CASE(4)
+    RA_MFMA_CASE(8)
+#undef RA_MFMA_CASE
+    RA_LAUNCH_CHECK("tile_mfma_kernel");
+    return RA_OK;
+}
+
+template <int KIND>
+ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, float* scratch, int N,
+                           hipStream_t st) {
+    const int M = p->info.M;
+    const Items it = plan_items(p);
+    const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
+    const bool vec = (N % F == 0) && ((reinterpret_cast<uintptr_t>(B) % (4 * F)) == 0);
+    dim3 grid((p->num_items + kWavesPerBlock - 1) / kWavesPerBlock, (N + 64 * F - 1) / (64 * F));
+    const int bf = p->info.value_dtype == RA_DTYPE_BF16;
+    const int32_t* ax = p->atox.get<int32_t>();
+    const uint16_t* vl = p->vals.get<uint16_t>();
+#define RA_FP32_CASE(f)                                                                              \
+    if (F == f) {                                                                                    \
+        if (vec)                                                                                     \
+            tile_fp32_kernel<f, true, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, B, C, scratch, M, N, \
+                                                                   p->num_items);                   \
+        else                                                                                         \
+            tile_fp32_kernel<f, false, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, B, C, scratch, M, N, \
+                                                                    p->num_items);                  \
+    }
+    RA_FP32_CASE(1)
+    RA_FP32_CASE(2)
+    RA_FP32_CASE(4)
+#undef RA_FP32_CASE
+    RA_LAUNCH_CHECK("tile_fp32_kernel");
+    return RA_OK;
+}
+
+ra_status launch_merge(const ra_tile_plan* p, float* C, int N, hipStream_t st) {
+    if (p->info.num_split_windows == 0) return RA_OK;
+    dim3 grid(p->info.num_split_windows, (8 * N + kBlock - 1) / kBlock);
+    tile_merge_kernel<<<grid, kBlock, 0, st>>>(p->split_windows.get<int32_t>(),
+                                               p->split_offsets.get<int32_t>(),
+                                               p->scratch.get<float>(), C, p->info.M, N);
+    RA_LAUNCH_CHECK("tile_merge_kernel");
+    return RA_OK;
+}
+
+ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* B32, bool bf16,
+                     bool fp32_route, float* C, int N, hipStream_t st) {
+    float* scratch = nullptr;
+    if (p->info.kind == RA_TILE_SEGMENT_HYBRID && p->info.num_split_segs > 0) {
+        RA_TRY(p->scratch.ensure((size_t)p->info.num_split_segs * ra::kTileWindow * N * sizeof(float)));
+        scratch = p->scratch.get<float>();
+    }
+    switch (p->info.kind) {
+        case RA_TILE_TC_DIRECT:
+            RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_TC_DIRECT>(p, B32, C, scratch, N, st)
+                              : launch_mfma_kind<RA_TILE_TC_DIRECT>(p, Bh, ldb, bf16, C, scratch, N, st));
+            break;
+        case RA_TILE_COMMUNITY_TC:
+            RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_COMMUNITY_TC>(p, B32, C, scratch, N, st)
+                              : launch_mfma_kind<RA_TILE_COMMUNITY_TC>(p, Bh, ldb, bf16, C, scratch, N, st));
+            break;
+        default:
+            RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_SEGMENT_HYBRID>(p, B32, C, scratch, N, st)
+                              : launch_mfma_kind<RA_TILE_SEGMENT_HYBRID>(p, Bh, ldb, bf16, C, scratch, N, st));
+            RA_TRY(launch_merge(p, C, N, st));
+            break;
+    }
+    return RA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+ra_status ra_convert_f32(const float* d_in, void* d_out, int64_t rows, int32_t cols, int32_t ldo,
+                         int32_t out_dtype, ra_stream_t stream) {
+    if (rows < 0 || cols < 0 || ldo < cols || (ldo % 8) != 0)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "convert: need ldo >= cols and ldo % 8 == 0");
+    if (out_dtype != RA_DTYPE_F16 && out_dtype != RA_DTYPE_BF16)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "convert: out_dtype must be F16 or BF16");
+    if (rows > 0 && (!d_in || !d_out)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "convert: NULL buffer");
+    if (!ra::aligned16(d_out)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "convert: output not 16-byte aligned");
+    return launch_convert(d_in, d_out, rows, cols, ldo, out_dtype == RA_DTYPE_BF16,
+                          reinterpret_cast<hipStream_t>(stream));
+}
+
+ra_status ra_tile_plan_create(int32_t kind, const int32_t* h_rowptr, const int32_t* h_colind,
+                              const float* h_vals, int32_t M, int32_t K, int32_t N,
+                              int32_t value_dtype, ra_tile_plan** out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: out is NULL");
+    *out = nullptr;
+    const auto t0 = std::chrono::steady_clock::now();
+    ra_tile_host host;
+    try {
+        RA_TRY(ra::tile_host_build(kind, h_rowptr, h_colind, h_vals, M, K, N, value_dtype, host));
+    } catch (const std::bad_alloc&) {
+        return ra::fail(RA_ERR_OUT_OF_MEMORY, "tile: host build out of memory");
+    }
+    auto p = new (std::nothrow) ra_tile_plan();
+    if (!p) return ra::fail(RA_ERR_OUT_OF_MEMORY, "tile: plan allocation");
+    ra_status s = ra_tile_host_get_info(&host, &p->info);
+    if (s == RA_OK && host.active) {
+        if ((s = p->block_offsets.upload(host.block_offsets)) == RA_OK &&
+            (s = p->atox.upload(host.atox)) == RA_OK && (s = p->vals.upload(host.vals)) == RA_OK &&
+            (s = p->win_rows.upload(host.win_rows)) == RA_OK &&
+            (s = p->seg_window.upload(host.seg_window)) == RA_OK &&
+            (s = p->seg_bbegin.upload(host.seg_bbegin)) == RA_OK &&
+            (s = p->seg_bend.upload(host.seg_bend)) == RA_OK &&
+            (s = p->seg_slot.upload(host.seg_slot)) == RA_OK &&
+            (s = p->split_windows.upload(host.split_windows)) == RA_OK &&
+            (s = p->split_offsets.upload(host.split_offsets)) == RA_OK) {
+            p->num_items = kind == RA_TILE_SEGMENT_HYBRID ? p->info.num_segments : p->info.num_windows;
+        }
+    }
+    if (s != RA_OK) {
+        delete p;
+        return s;
+    }
+    p->info.build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    *out = p;
+    return RA_OK;
+}
+
+ra_status ra_tile_plan_run(ra_tile_plan* p, const float* d_B, float* d_C, int32_t N, int32_t route,
+                           ra_stream_t stream) {
+    if (!p) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: plan is NULL");
+    if (!p->info.active)
+        return ra::fail(RA_ERR_INACTIVE_PLAN, "tile: plan is inactive (built with N < 16 or empty matrix)");
+    if (N <= 0 || p->info.M == 0) return RA_OK;
+    if (!d_B || !d_C) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: NULL B or C");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (route == RA_TILE_ROUTE_FP32) return run_common(p, nullptr, 0, d_B, false, true, d_C, N, st);
+    if (route != RA_TILE_ROUTE_F16 && route != RA_TILE_ROUTE_BF16)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: unknown route");
+    const bool bf16 = route == RA_TILE_ROUTE_BF16;
+    if (bf16 != (p->info.value_dtype == RA_DTYPE_BF16))
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: route precision differs from the plan's value dtype");
+    const int ldb = (N + 7) / 8 * 8;
+    RA_TRY(p->bconv.ensure((size_t)p->info.K * ldb * sizeof(uint16_t)));
+    RA_TRY(launch_convert(d_B, p->bconv.get(), p->info.K, N, ldb, bf16, st));
+    return run_common(p, p->bconv.get<uint16_t>(), ldb, nullptr, bf16, false, d_C, N, st);
+}
+
+ra_status ra_tile_plan_run_lowp(ra_tile_plan* p, const void* d_Bh, int32_t ldb, int32_t b_dtype,
+                                float* d_C, int32_t N, ra_stream_t stream) {
+    if (!p) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: plan is NULL");
+    if (!p->info.active)
+        return ra::fail(RA_ERR_INACTIVE_PLAN, "tile: plan is inactive (built with N < 16 or empty matrix)");
+    if (N <= 0 || p->info.M == 0) return RA_OK;
+    if (!d_Bh || !d_C) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: NULL B or C");
+    if (ldb < N || (ldb % 8) != 0 || !ra::aligned16(d_Bh))
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: low-precision B needs ldb >= N, ldb % 8 == 0, 16-byte alignment");
+    const bool bf16 = b_dtype == RA_DTYPE_BF16;
+    if (b_dtype != RA_DTYPE_F16 && !bf16) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: b_dtype must be F16 or BF16");
+    if (bf16 != (p->info.value_dtype == RA_DTYPE_BF16))
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: B precision differs from the plan's value dtype");
+    return run_common(p, static_cast<const uint16_t*>(d_Bh), ldb, nullptr, bf16, false, d_C, N,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+ra_status ra_tile_plan_get_info(const ra_tile_plan* p, ra_tile_info* info) {
+    if (!p || !info) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: NULL argument");
+    *info = p->info;
+    return RA_OK;
+}
+
+void ra_tile_plan_destroy(ra_tile_plan* p) { delete p; }
+
+}  // extern "C"

@@ -1,0 +1,530 @@
+// torch_binding.cpp — the `ra_spmm` extension surface over the C ABI.
+//
+// Mirrors the deployed subset of the reference pybind module
+// (bindings/ra_bindings.cpp:2318-2899): same function names, keyword names,
+// argument meaning, plan classes and RuntimeError behaviour.  Everything here
+// is marshalling: tensor checks, C allocation, plan ownership and dicts.  All
+// compute goes through include/ra_spmm.h; launches use the current torch
+// stream (the reference used the legacy default stream for its CSR kernels and
+// the current stream for its tile kernels, bindings/ra_bindings.cpp:2164).
+#include <torch/extension.h>
+#include <c10/hip/HIPStream.h>
+
+#include <chrono>
+#include <memory>
+#include <string>
+
+#include "../../include/ra_spmm.h"
+
+namespace {
+
+ra_stream_t current_stream() {
+    return reinterpret_cast<ra_stream_t>(c10::hip::getCurrentHIPStream().stream());
+}
+
+void check(ra_status s, const char* what) {
+    TORCH_CHECK(s == RA_OK, what, " failed: ", ra_status_string(s), ": ", ra_last_error());
+}
+
+// bindings/ra_bindings.cpp:288-306
+void check_gpu_tensor(const torch::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+void check_dense_float(const torch::Tensor& t, const char* name) {
+    check_gpu_tensor(t, name);
+    TORCH_CHECK(t.scalar_type() == torch::kFloat32, name, " must be float32");
+    TORCH_CHECK(t.dim() == 2, name, " must be 2-D");
+}
+void check_csr(const torch::Tensor& rowptr, const torch::Tensor& colind, const torch::Tensor& vals) {
+    check_gpu_tensor(rowptr, "rowptr");
+    check_gpu_tensor(colind, "colind");
+    check_gpu_tensor(vals, "vals");
+    TORCH_CHECK(rowptr.scalar_type() == torch::kInt32, "rowptr must be int32");
+    TORCH_CHECK(colind.scalar_type() == torch::kInt32, "colind must be int32");
+    TORCH_CHECK(vals.scalar_type() == torch::kFloat32, "vals must be float32");
+    TORCH_CHECK(rowptr.dim() == 1 && rowptr.numel() >= 1, "rowptr must be 1-D with M+1 entries");
+}
+void check_same_device(const torch::Tensor& a, const torch::Tensor& b) {
+    TORCH_CHECK(a.device() == b.device(), "tensors must be on the same device");
+}
+
+torch::Tensor host_i32(const torch::Tensor& t) { return t.cpu().contiguous().to(torch::kInt32); }
+torch::Tensor host_f32(const torch::Tensor& t) { return t.cpu().contiguous().to(torch::kFloat32); }
+
+// ------------------------------------------------------------ CSR_DIRECT
+torch::Tensor spmm_csr_direct(torch::Tensor rowptr, torch::Tensor colind, torch::Tensor vals,
+                              torch::Tensor B) {
+    check_csr(rowptr, colind, vals);
+    check_dense_float(B, "B");
+    check_same_device(rowptr, B);
+    const int M = static_cast<int>(rowptr.size(0)) - 1;
+    const int K = static_cast<int>(B.size(0));
+    const int N = static_cast<int>(B.size(1));
+    auto C = torch::empty({M, N}, B.options());
+    check(ra_spmm_csr_direct(rowptr.data_ptr<int32_t>(), colind.data_ptr<int32_t>(),
+                             vals.data_ptr<float>(), B.data_ptr<float>(), C.data_ptr<float>(), M,
+                             K, N, colind.numel(), current_stream()),
+          "spmm_csr_direct");
+    return C;
+}
+
+// --------------------------------------------------- baseline (guardrail)
+torch::Tensor spmm_csr_baseline(torch::Tensor rowptr, torch::Tensor colind, torch::Tensor vals,
+                                torch::Tensor B) {
+    check_csr(rowptr, colind, vals);
+    check_dense_float(B, "B");
+    check_same_device(rowptr, B);
+    const int M = static_cast<int>(rowptr.size(0)) - 1;
+    const int K = static_cast<int>(B.size(0));
+    const int N = static_cast<int>(B.size(1));
+    auto C = torch::empty({M, N}, B.options());
+    check(ra_spmm_csr_baseline(rowptr.data_ptr<int32_t>(), colind.data_ptr<int32_t>(),
+                               vals.data_ptr<float>(), B.data_ptr<float>(), C.data_ptr<float>(),
+                               M, K, N, colind.numel(), current_stream()),
+          "spmm_csr_baseline");
+    return C;
+}
+
+// Reusable guardrail plan: keeps the CSR tensors and owns its output, like the
+// reference CuSparsePlanWrapper (bindings/ra_bindings.cpp:620-631, 1025-1037):
+// run_cusparse_plan writes into and returns the same C every call.
+struct BaselinePlan {
+    torch::Tensor rowptr, colind, vals, C;
+    int64_t K = 0, N = 0;
+};
+
+std::shared_ptr<BaselinePlan> make_cusparse_plan(torch::Tensor rowptr, torch::Tensor colind,
+                                                 torch::Tensor vals, torch::Tensor B) {
+    check_csr(rowptr, colind, vals);
+    check_dense_float(B, "B");
+    auto p = std::make_shared<BaselinePlan>();
+    p->rowptr = rowptr;
+    p->colind = colind;
+    p->vals = vals;
+    p->K = B.size(0);
+    p->N = B.size(1);
+    p->C = torch::zeros({rowptr.size(0) - 1, B.size(1)}, B.options());
+    return p;
+}
+
+torch::Tensor run_cusparse_plan(std::shared_ptr<BaselinePlan> p, torch::Tensor B) {
+    TORCH_CHECK(p, "Invalid cuSPARSE plan");
+    check_dense_float(B, "B");
+    TORCH_CHECK(B.size(0) == p->K && B.size(1) == p->N, "cuSPARSE plan expects B shape [", p->K,
+                ", ", p->N, "], got [", B.size(0), ", ", B.size(1), "]");
+    const int M = static_cast<int>(p->rowptr.size(0)) - 1;
+    check(ra_spmm_csr_baseline(p->rowptr.data_ptr<int32_t>(), p->colind.data_ptr<int32_t>(),
+                               p->vals.data_ptr<float>(), B.data_ptr<float>(),
+                               p->C.data_ptr<float>(), M, static_cast<int>(p->K),
+                               static_cast<int>(p->N), p->colind.numel(), current_stream()),
+          "run_cusparse_plan");
+    return p->C;
+}
+
+// ------------------------------------------------------------- features
+ra_features features_of(const torch::Tensor& rowptr, int M, int K, int N, const char** backend) {
+    ra_features f{};
+    TORCH_CHECK(rowptr.numel() >= M + 1, "rowptr has fewer than M+1 entries");
+    if (rowptr.is_cuda()) {
+        TORCH_CHECK(rowptr.scalar_type() == torch::kInt32 && rowptr.is_contiguous(),
+                    "device rowptr must be contiguous int32");
+        check(ra_features_device(rowptr.data_ptr<int32_t>(), M, K, N, current_stream(), &f),
+              "features");
+        *backend = "cuda_rowptr_moments";
+    } else {
+        auto rp = host_i32(rowptr);
+        check(ra_features_host(rp.data_ptr<int32_t>(), M, K, N, &f), "features");
+        *backend = "cpu_rowptr_moments";
+    }
+    return f;
+}
+
+int parse_table(const std::string& table) {
+    if (table == "mi355x" || table == "MI355X") return RA_TABLE_MI355X;
+    if (table == "reference" || table == "REFERENCE") return RA_TABLE_REFERENCE;
+    TORCH_CHECK(false, "unknown router table '", table, "' (expected 'mi355x' or 'reference')");
+    return -1;
+}
+
+pybind11::dict features_to_dict(const ra_features& f) {
+    pybind11::dict d;
+    d["M"] = f.M;
+    d["K"] = f.K;
+    d["N"] = f.N;
+    d["nnz"] = f.nnz;
+    d["sum_deg_sq"] = f.sum_deg_sq;
+    d["max_deg"] = f.max_deg;
+    d["empty_rows"] = f.empty_rows;
+    d["avg"] = f.avg;
+    d["std"] = f.std_dev;
+    d["avg_nnz_per_row"] = f.avg_nnz_per_row;
+    d["std_nnz_per_row"] = f.std_nnz_per_row;
+    d["degree_cv"] = f.degree_cv;
+    d["max_to_mean_ratio"] = f.max_to_mean_ratio;
+    return d;
+}
+
+// bindings/ra_bindings.cpp:634-718 (plan_to_dict) + :1717-1753 (make_router_plan_fn)
+pybind11::dict route_to_dict(const ra_features& f, const ra_route& r, float ms) {
+    pybind11::dict d;
+    d["chosen_path"] = std::string(ra_path_name(r.chosen_path));
+    d["use_tf32"] = static_cast<bool>(r.use_tf32);
+    d["chosen_path_int"] = r.chosen_path;
+    d["decision_reason"] = std::string(r.decision_reason);
+    d["matched_rule"] = r.rule;
+    d["estimated_risk"] = r.estimated_risk;
+    d["planning_time_ms"] = ms;
+    d["gate_margin_raw"] = 0.0f;
+    d["gate_margin_norm"] = 0.0f;
+    d["est_plan_s"] = r.est_plan_s;
+    d["tile_ok"] = static_cast<bool>(r.tile_ok);
+    d["path_count"] = static_cast<int>(RA_PATH_COUNT);
+    pybind11::list names, feas;
+    pybind11::dict by_path, codes, details;
+    for (int p = 0; p < RA_PATH_COUNT; ++p) {
+        const std::string name = ra_path_name(p);
+        names.append(name);
+        feas.append(static_cast<bool>(r.feasible[p]));
+        by_path[name.c_str()] = static_cast<bool>(r.feasible[p]);
+        codes[name.c_str()] = std::string(ra_reject_name(r.rejection_code[p]));
+        std::string detail;
+        if (r.rejection_code[p] == RA_REJECT_MARGIN_TOO_SMALL) detail = "N < 16";
+        else if (r.rejection_code[p] == RA_REJECT_NOT_FEASIBLE) detail = "not built for MI355X";
+        else if (r.rejection_code[p] == RA_REJECT_NOT_IN_PORTFOLIO) detail = name + " not in selected portfolio";
+        details[name.c_str()] = detail;
+    }
+    d["path_names"] = names;
+    d["feasible"] = feas;
+    d["feasible_by_path"] = by_path;
+    d["rejection_codes"] = codes;
+    d["rejection_details"] = details;
+    pybind11::dict fv = features_to_dict(f);
+    d["feature_values"] = fv;
+    pybind11::dict scores;  // diagnostic-only in the reference (router_scores.cpp)
+    for (const char* k : {"csr_direct", "csr_adaptive", "staged_reuse", "tc_sparse",
+                          "row_split_cuda", "tc_reordered", "hybrid_tc_cuda", "cusparse"})
+        scores[k] = 0.0f;
+    d["scores"] = scores;
+    return d;
+}
+
+pybind11::dict make_router_plan(torch::Tensor rowptr, torch::Tensor colind, torch::Tensor vals,
+                                int M, int K, int N, std::string portfolio, std::string table) {
+    const auto t0 = std::chrono::high_resolution_clock::now();
+    const int port = (portfolio == "FULL") ? RA_PORTFOLIO_FULL : RA_PORTFOLIO_MAIN;
+    const char* backend = "";
+    ra_features f = features_of(rowptr, M, K, N, &backend);
+    ra_route r{};
+    check(ra_route_dispatch(&f, port, parse_table(table), &r), "route_dispatch");
+    const auto t1 = std::chrono::high_resolution_clock::now();
+    pybind11::dict d =
+        route_to_dict(f, r, std::chrono::duration<float, std::milli>(t1 - t0).count());
+    d["feature_set"] = "production_4";
+    d["feature_backend"] = backend;
+    d["router_table"] = table;
+    (void)colind;
+    (void)vals;
+    return d;
+}
+
+pybind11::dict compute_features(torch::Tensor rowptr, int M, int K, int N) {
+    const char* backend = "";
+    ra_features f = features_of(rowptr, M, K, N, &backend);
+    pybind11::dict d = features_to_dict(f);
+    d["feature_backend"] = backend;
+    return d;
+}
+
+pybind11::dict route_features(int M, int K, int N, int64_t nnz, int64_t sum_deg_sq, int max_deg,
+                              int64_t empty_rows, std::string portfolio, std::string table) {
+    ra_features f{};
+    check(ra_features_from_moments(M, K, N, nnz, sum_deg_sq, max_deg, empty_rows, &f), "features");
+    ra_route r{};
+    check(ra_route_dispatch(&f, portfolio == "FULL" ? RA_PORTFOLIO_FULL : RA_PORTFOLIO_MAIN,
+                            parse_table(table), &r),
+          "route_dispatch");
+    pybind11::dict d = route_to_dict(f, r, 0.f);
+    d["router_table"] = table;
+    return d;
+}
+
+// --------------------------------------------------- ZERO_OVERHEAD_CSR
+struct ZOPlan {
+    ra_zo_plan* plan = nullptr;
+    ra_zo_info info{};
+    bool valid = false;
+    ~ZOPlan() { ra_zo_plan_destroy(plan); }
+};
+
+std::shared_ptr<ZOPlan> make_zero_overhead_plan(torch::Tensor rowptr_cpu, int M, int K) {
+    auto rp = host_i32(rowptr_cpu);
+    TORCH_CHECK(rp.numel() >= M + 1, "rowptr has fewer than M+1 entries");
+    auto w = std::make_shared<ZOPlan>();
+    check(ra_zo_plan_create(rp.data_ptr<int32_t>(), M, K, &w->plan), "make_zero_overhead_plan");
+    check(ra_zo_plan_get_info(w->plan, &w->info), "zero_overhead info");
+    w->valid = true;
+    return w;
+}
+
+torch::Tensor run_zero_overhead_plan(std::shared_ptr<ZOPlan> w, torch::Tensor rowptr,
+                                     torch::Tensor colind, torch::Tensor vals, torch::Tensor B) {
+    check_gpu_tensor(rowptr, "rowptr");
+    check_gpu_tensor(colind, "colind");
+    check_gpu_tensor(vals, "vals");
+    check_dense_float(B, "B");
+    TORCH_CHECK(w && w->valid, "Invalid ZeroOverhead plan");
+    TORCH_CHECK(rowptr.scalar_type() == torch::kInt32 && colind.scalar_type() == torch::kInt32 &&
+                    vals.scalar_type() == torch::kFloat32,
+                "rowptr/colind must be int32 and vals float32");
+    const int M = w->info.M;
+    const int N = static_cast<int>(B.size(1));
+    auto C = torch::empty({M, N}, B.options());
+    check(ra_zo_plan_run(w->plan, rowptr.data_ptr<int32_t>(), colind.data_ptr<int32_t>(),
+                         vals.data_ptr<float>(), B.data_ptr<float>(), C.data_ptr<float>(), N,
+                         current_stream()),
+          "run_zero_overhead_plan");
+    return C;
+}
+
+// Stage-timing hook: writes into a caller-provided C (see ra_zo_plan_run_stage).
+void run_zero_overhead_plan_stage(std::shared_ptr<ZOPlan> w, torch::Tensor rowptr,
+                                  torch::Tensor colind, torch::Tensor vals, torch::Tensor B,
+                                  torch::Tensor C, int stage) {
+    TORCH_CHECK(w && w->valid, "Invalid ZeroOverhead plan");
+    check_dense_float(B, "B");
+    check_dense_float(C, "C");
+    TORCH_CHECK(C.size(0) == w->info.M && C.size(1) == B.size(1), "C must be [M, N]");
+    check(ra_zo_plan_run_stage(w->plan, rowptr.data_ptr<int32_t>(), colind.data_ptr<int32_t>(),
+                               vals.data_ptr<float>(), B.data_ptr<float>(), C.data_ptr<float>(),
+                               static_cast<int>(B.size(1)), stage, current_stream()),
+          "run_zero_overhead_plan_stage");
+}
+
+// --------------------------------------------------------- tile family
+struct TilePlan {
+    ra_tile_plan* plan = nullptr;
+    ra_tile_info info{};
+    bool valid = false;
+    ~TilePlan() { ra_tile_plan_destroy(plan); }
+};
+
+int parse_value_dtype(const std::string& s) {
+    if (s == "fp16" || s == "float16" || s == "half") return RA_DTYPE_F16;
+    if (s == "bf16" || s == "bfloat16") return RA_DTYPE_BF16;
+    TORCH_CHECK(false, "value_dtype must be 'fp16' or 'bf16', got '", s, "'");
+    return -1;
+}
+
+std::shared_ptr<TilePlan> make_tile_plan(int kind, torch::Tensor rowptr_cpu, torch::Tensor colind_cpu,
+                                         torch::Tensor vals_cpu, int M, int K, int N,
+                                         const std::string& value_dtype, const char* what) {
+    auto rp = host_i32(rowptr_cpu);
+    auto ci = host_i32(colind_cpu);
+    auto vl = host_f32(vals_cpu);
+    TORCH_CHECK(rp.numel() >= M + 1, "rowptr has fewer than M+1 entries");
+    auto w = std::make_shared<TilePlan>();
+    check(ra_tile_plan_create(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
+                              vl.data_ptr<float>(), M, K, N, parse_value_dtype(value_dtype),
+                              &w->plan),
+          what);
+    check(ra_tile_plan_get_info(w->plan, &w->info), "tile info");
+    w->valid = true;
+    return w;
+}
+
+torch::Tensor run_tile_plan(const std::shared_ptr<TilePlan>& w, const torch::Tensor& B, int route,
+                            const char* what) {
+    TORCH_CHECK(w && w->valid, "Invalid tile plan");
+    check_gpu_tensor(B, "B");
+    TORCH_CHECK(B.dim() == 2, "B must be 2-D");
+    const int M = w->info.M;
+    const int N = static_cast<int>(B.size(1));
+    auto C = torch::empty({M, N}, B.options().dtype(torch::kFloat32));
+    if (B.scalar_type() == torch::kFloat32) {
+        check(ra_tile_plan_run(w->plan, B.data_ptr<float>(), C.data_ptr<float>(), N, route,
+                               current_stream()),
+              what);
+    } else {
+        TORCH_CHECK(B.scalar_type() == torch::kFloat16 || B.scalar_type() == torch::kBFloat16,
+                    "B must be float32, float16 or bfloat16");
+        TORCH_CHECK(N % 8 == 0, "fp16/bf16 B needs N % 8 == 0 (pass float32 B otherwise)");
+        check(ra_tile_plan_run_lowp(w->plan, B.data_ptr(), N,
+                                    B.scalar_type() == torch::kFloat16 ? RA_DTYPE_F16 : RA_DTYPE_BF16,
+                                    C.data_ptr<float>(), N, current_stream()),
+              what);
+    }
+    return C;
+}
+
+int half_route(const TilePlan& w) {
+    // The low-precision route follows the plan's stored value type.
+    return w.info.value_dtype == RA_DTYPE_BF16 ? RA_TILE_ROUTE_BF16 : RA_TILE_ROUTE_F16;
+}
+
+void bind_tile_props(pybind11::class_<TilePlan, std::shared_ptr<TilePlan>>& c) {
+    c.def_property_readonly("valid", [](const TilePlan& w) { return w.valid; })
+        .def_property_readonly("active", [](const TilePlan& w) { return w.info.active != 0; })
+        .def_property_readonly("M", [](const TilePlan& w) { return w.info.M; })
+        .def_property_readonly("K", [](const TilePlan& w) { return w.info.K; })
+        .def_property_readonly("nnz", [](const TilePlan& w) { return w.info.nnz; })
+        .def_property_readonly("num_windows", [](const TilePlan& w) { return w.info.num_windows; })
+        .def_property_readonly("num_tc_tiles", [](const TilePlan& w) { return w.info.num_blocks; })
+        .def_property_readonly("num_vectors", [](const TilePlan& w) { return w.info.num_vectors; })
+        .def_property_readonly("avg_tc_tile_density",
+                               [](const TilePlan& w) { return w.info.avg_tile_density; })
+        .def_property_readonly("plan_bytes", [](const TilePlan& w) { return w.info.plan_bytes; })
+        .def_property_readonly("build_ms", [](const TilePlan& w) { return w.info.build_ms; });
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_C, m) {
+    m.doc() = "MI355X-native regime-aware SpMM (ra_spmm) — HIP kernels for gfx950";
+
+    m.def("spmm_csr_direct", &spmm_csr_direct, "CSR_DIRECT SpMM (lane group per row, wave64)",
+          pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"),
+          pybind11::arg("B"));
+    m.def("spmm_csr_baseline", &spmm_csr_baseline,
+          "Regime-free baseline CSR SpMM (one wavefront per row)", pybind11::arg("rowptr"),
+          pybind11::arg("colind"), pybind11::arg("vals"), pybind11::arg("B"));
+
+    // Guardrail names of the reference, served by the baseline CSR kernel.
+    m.def("spmm_cusparse", &spmm_csr_baseline,
+          "Guardrail SpMM (served by the hand-written baseline CSR kernel)",
+          pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"),
+          pybind11::arg("B"));
+    pybind11::class_<BaselinePlan, std::shared_ptr<BaselinePlan>>(m, "CuSparsePlan")
+        .def_property_readonly("algorithm",
+                               [](const BaselinePlan&) { return std::string("RA_BASELINE_CSR_WAVE_PER_ROW"); });
+    m.def("make_cusparse_plan", &make_cusparse_plan, "Reusable guardrail plan (owns C)",
+          pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"),
+          pybind11::arg("B"));
+    m.def("run_cusparse_plan", &run_cusparse_plan, "Run a reusable guardrail plan",
+          pybind11::arg("plan"), pybind11::arg("B"));
+
+    m.def("make_router_plan", &make_router_plan,
+          "Four-feature MAIN router plan (features on the GPU when rowptr is a device tensor)",
+          pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"),
+          pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"),
+          pybind11::arg("portfolio") = "MAIN", pybind11::arg("table") = "mi355x");
+    m.def("compute_features", &compute_features, "Production routing features of a rowptr",
+          pybind11::arg("rowptr"), pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"));
+    m.def("route_features", &route_features,
+          "Route from exact integer moments (CPU only; no tensors)", pybind11::arg("M"),
+          pybind11::arg("K"), pybind11::arg("N"), pybind11::arg("nnz"), pybind11::arg("sum_deg_sq"),
+          pybind11::arg("max_deg"), pybind11::arg("empty_rows"), pybind11::arg("portfolio") = "MAIN",
+          pybind11::arg("table") = "mi355x");
+
+    pybind11::class_<ZOPlan, std::shared_ptr<ZOPlan>>(m, "RAZeroOverheadPlan")
+        .def_property_readonly("valid", [](const ZOPlan& w) { return w.valid; })
+        .def_property_readonly("M", [](const ZOPlan& w) { return w.info.M; })
+        .def_property_readonly("K", [](const ZOPlan& w) { return w.info.K; })
+        .def_property_readonly("num_tiny", [](const ZOPlan& w) { return w.info.num_tiny; })
+        .def_property_readonly("num_short", [](const ZOPlan& w) { return w.info.num_short; })
+        .def_property_readonly("num_medium", [](const ZOPlan& w) { return w.info.num_medium; })
+        .def_property_readonly("num_long", [](const ZOPlan& w) { return w.info.num_long; })
+        .def_property_readonly("num_empty", [](const ZOPlan& w) { return w.info.num_empty; })
+        .def_property_readonly("num_chunks", [](const ZOPlan& w) { return w.info.num_chunks; })
+        .def_property_readonly("num_split_rows", [](const ZOPlan& w) { return w.info.num_split_rows; })
+        .def_property_readonly("max_long_chunks", [](const ZOPlan& w) { return w.info.max_long_chunks; })
+        .def_property_readonly("num_split_chunks", [](const ZOPlan& w) { return w.info.num_split_chunks; })
+        .def_property_readonly("plan_bytes", [](const ZOPlan& w) { return w.info.plan_bytes; });
+    m.def("make_zero_overhead_plan", &make_zero_overhead_plan,
+          "Build the ZERO_OVERHEAD_CSR plan (degree-binned dispatch)", pybind11::arg("rowptr_cpu"),
+          pybind11::arg("M"), pybind11::arg("K"));
+    m.def("run_zero_overhead_plan", &run_zero_overhead_plan, "Run ZERO_OVERHEAD_CSR SpMM",
+          pybind11::arg("plan"), pybind11::arg("rowptr"), pybind11::arg("colind"),
+          pybind11::arg("vals"), pybind11::arg("B"));
+
+    m.def("run_zero_overhead_plan_stage", &run_zero_overhead_plan_stage,
+          "Run one ZERO_OVERHEAD_CSR launch stage into C (1 = fused kernel, 2 = merge, 0 = both)",
+          pybind11::arg("plan"), pybind11::arg("rowptr"), pybind11::arg("colind"),
+          pybind11::arg("vals"), pybind11::arg("B"), pybind11::arg("C"), pybind11::arg("stage"));
+
+    auto tc = pybind11::class_<TilePlan, std::shared_ptr<TilePlan>>(m, "RATilePlan");
+    bind_tile_props(tc);
+    tc.def_property_readonly("num_groups", [](const TilePlan& w) { return w.info.num_windows; })
+        .def_property_readonly("num_communities", [](const TilePlan& w) { return w.info.num_windows; })
+        .def_property_readonly("num_tc_groups", [](const TilePlan& w) { return w.info.num_windows; })
+        .def_property_readonly("num_segments", [](const TilePlan& w) { return w.info.num_segments; })
+        .def_property_readonly("num_split_windows", [](const TilePlan& w) { return w.info.num_split_windows; })
+        .def_property_readonly("num_fp32_rows", [](const TilePlan&) { return 0; })
+        .def_property_readonly("fp32_group_fraction", [](const TilePlan&) { return 0.0f; })
+        .def_property_readonly("intra_community_nnz_fraction",
+                               [](const TilePlan& w) { return w.info.avg_tile_density; })
+        .def_property_readonly("tc_nnz_fraction", [](const TilePlan&) { return 1.0f; })
+        .def_property_readonly("cuda_nnz_fraction", [](const TilePlan&) { return 0.0f; })
+        .def_property_readonly("kind", [](const TilePlan& w) { return w.info.kind; });
+    // The reference exposes one class per family; they share one layout here.
+    m.attr("RATcDirectPlan") = tc;
+    m.attr("RACommunityTCPlan") = tc;
+    m.attr("RASegmentHybridPlan") = tc;
+
+    struct Fam {
+        const char* make;
+        const char* run;
+        const char* run32;
+        int kind;
+    };
+    for (const Fam& f : {Fam{"make_tc_direct_plan", "run_tc_direct_plan", "run_tc_direct_plan_tf32",
+                             RA_TILE_TC_DIRECT},
+                         Fam{"make_community_tc_plan", "run_community_tc_plan",
+                             "run_community_tc_plan_tf32", RA_TILE_COMMUNITY_TC},
+                         Fam{"make_segment_hybrid_plan", "run_segment_hybrid_plan",
+                             "run_segment_hybrid_plan_tf32", RA_TILE_SEGMENT_HYBRID}}) {
+        const int kind = f.kind;
+        const std::string make_name = f.make;
+        m.def(f.make,
+              [kind, make_name](torch::Tensor rp, torch::Tensor ci, torch::Tensor vl, int M, int K,
+                                int N, std::string value_dtype) {
+                  return make_tile_plan(kind, rp, ci, vl, M, K, N, value_dtype, make_name.c_str());
+              },
+              "Build the tile plan (host build + upload)", pybind11::arg("rowptr_cpu"),
+              pybind11::arg("colind_cpu"), pybind11::arg("vals_cpu"), pybind11::arg("M"),
+              pybind11::arg("K"), pybind11::arg("N"), pybind11::arg("value_dtype") = "fp16");
+        if (kind == RA_TILE_SEGMENT_HYBRID) {
+            // run_segment_hybrid_plan(plan, colind, vals, B): colind/vals are kept
+            // for ABI compatibility, as in tc/ra_segment_hybrid.cu:546-551.
+            m.def(f.run,
+                  [](std::shared_ptr<TilePlan> w, torch::Tensor, torch::Tensor, torch::Tensor B) {
+                      return run_tile_plan(w, B, half_route(*w),
+                                           "run_segment_hybrid_plan");
+                  },
+                  "Run on the FP16/BF16 MFMA route", pybind11::arg("plan"), pybind11::arg("colind"),
+                  pybind11::arg("vals"), pybind11::arg("B"));
+            m.def(f.run32,
+                  [](std::shared_ptr<TilePlan> w, torch::Tensor, torch::Tensor, torch::Tensor B) {
+                      return run_tile_plan(w, B, RA_TILE_ROUTE_FP32, "run_segment_hybrid_plan_tf32");
+                  },
+                  "Run on the FP32-FMA route (replaces the TF32 path)", pybind11::arg("plan"),
+                  pybind11::arg("colind"), pybind11::arg("vals"), pybind11::arg("B"));
+        } else {
+            const std::string rn = f.run, rn32 = f.run32;
+            m.def(f.run,
+                  [rn](std::shared_ptr<TilePlan> w, torch::Tensor B) {
+                      return run_tile_plan(w, B, half_route(*w),
+                                           rn.c_str());
+                  },
+                  "Run on the FP16/BF16 MFMA route", pybind11::arg("plan"), pybind11::arg("B"));
+            m.def(f.run32,
+                  [rn32](std::shared_ptr<TilePlan> w, torch::Tensor B) {
+                      return run_tile_plan(w, B, RA_TILE_ROUTE_FP32, rn32.c_str());
+                  },
+                  "Run on the FP32-FMA route (replaces the TF32 path)", pybind11::arg("plan"),
+                  pybind11::arg("B"));
+        }
+    }
+    m.def("run_tile_plan_route",
+          [](std::shared_ptr<TilePlan> w, torch::Tensor B, std::string route) {
+              int r = RA_TILE_ROUTE_F16;
+              if (route == "bf16") r = RA_TILE_ROUTE_BF16;
+              else if (route == "fp32") r = RA_TILE_ROUTE_FP32;
+              else TORCH_CHECK(route == "fp16", "route must be fp16, bf16 or fp32");
+              return run_tile_plan(w, B, r, "run_tile_plan_route");
+          },
+          "Run a tile plan on an explicit route", pybind11::arg("plan"), pybind11::arg("B"),
+          pybind11::arg("route"));
+
+    m.def("abi_version", &ra_abi_version);
+}

@@ -1,0 +1,40 @@
+"""ra_spmm — MI355X-native regime-aware SpMM (C = A @ B, A CSR, B dense).
+
+Drop-in for the reference `ra_spmm` extension (tariqaf/RA-SpMM,
+bindings/ra_bindings.cpp:2318-2899): the same plan/run functions, router dict
+and plan classes, backed by hand-written HIP kernels for gfx950 through the C
+ABI in include/ra_spmm.h.  There is no CPU fallback: importing fails loudly
+when the HIP extension is not built.
+"""
+from __future__ import annotations
+
+import torch  # noqa: F401  (loads the HIP runtime the extension binds to)
+
+try:
+    from . import _C
+except ImportError as exc:  # pragma: no cover - exercised only on broken installs
+    raise ImportError(
+        "ra_spmm: the HIP extension is not built; run `python ra-spmm_amd/build.py` "
+        f"(or __graft_entry__.build()). Original error: {exc}") from exc
+
+from ._C import (  # noqa: F401
+    CuSparsePlan, RACommunityTCPlan, RASegmentHybridPlan, RATcDirectPlan, RATilePlan,
+    RAZeroOverheadPlan, compute_features, make_community_tc_plan, make_cusparse_plan,
+    make_router_plan, make_segment_hybrid_plan, make_tc_direct_plan, make_zero_overhead_plan,
+    route_features, run_community_tc_plan, run_community_tc_plan_tf32, run_cusparse_plan,
+    run_segment_hybrid_plan, run_segment_hybrid_plan_tf32, run_tc_direct_plan,
+    run_tc_direct_plan_tf32, run_tile_plan_route, run_zero_overhead_plan, spmm_csr_baseline,
+    spmm_csr_direct, spmm_cusparse,
+)
+from .dispatch import (  # noqa: F401
+    DEPLOYED_KERNELS, TILE_KERNELS, benchmark_cusparse, benchmark_cusparse_cold,
+    build_kernel_plan, gpu_info_next, make_timing_breakdown, measure_exec_ms, measure_one_ms,
+    run_oracle_cold, run_oracle_warm, run_planned_kernel, run_router_cold, run_router_plan,
+    run_router_warm,
+)
+from .router import (  # noqa: F401
+    MI355X, REFERENCE, RouterTable, features_from_moments, production_features, route_label,
+    route_with_rules, simple_router,
+)
+
+__all__ = [n for n in dir() if not n.startswith("_")]

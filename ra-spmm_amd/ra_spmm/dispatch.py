@@ -1,0 +1,222 @@
+"""Label -> plan/run dispatch, timing drivers and one-shot helpers.
+
+Reference: build_kernel_plan / run_planned_kernel / benchmark_custom_cold,
+ra_real_graph_eval.py:247-343; make_timing_breakdown / measure_cuda_exec_ms,
+bench/benchmark.cpp:19-67; benchmark_cusparse[_cold], run_router_plan,
+run_router_{warm,cold}, run_oracle_{warm,cold}, bindings/ra_bindings.cpp:821-1037,
+1320-1965.  Timing uses HIP events on the current stream, which is the stream
+every ra_spmm launch goes to.
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+
+from . import _C
+from .router import route_label
+
+DEPLOYED_KERNELS = ["CSR_DIRECT", "ZERO_OVERHEAD_CSR", "TC_DIRECT", "COMMUNITY_TC",
+                    "SEGMENT_HYBRID", "TC_DIRECT_TF32", "COMMUNITY_TC_TF32",
+                    "SEGMENT_HYBRID_TF32"]
+TILE_KERNELS = {"TC_DIRECT", "COMMUNITY_TC", "SEGMENT_HYBRID", "TC_DIRECT_TF32",
+                "COMMUNITY_TC_TF32", "SEGMENT_HYBRID_TF32"}
+
+
+def build_kernel_plan(kernel_name, rowptr_cpu, colind_cpu, vals_cpu, M, K, N):
+    """ra_real_graph_eval.py:247-263."""
+    if kernel_name in ("CSR_DIRECT", "CSR_BASELINE"):
+        return None
+    if kernel_name == "ZERO_OVERHEAD_CSR":
+        return _C.make_zero_overhead_plan(rowptr_cpu, M, K)
+    if kernel_name in ("TC_DIRECT", "TC_DIRECT_TF32"):
+        return _C.make_tc_direct_plan(rowptr_cpu, colind_cpu, vals_cpu, M, K, N)
+    if kernel_name in ("COMMUNITY_TC", "COMMUNITY_TC_TF32"):
+        return _C.make_community_tc_plan(rowptr_cpu, colind_cpu, vals_cpu, M, K, N)
+    if kernel_name in ("SEGMENT_HYBRID", "SEGMENT_HYBRID_TF32"):
+        return _C.make_segment_hybrid_plan(rowptr_cpu, colind_cpu, vals_cpu, M, K, N)
+    raise ValueError(f"Kernel has no reusable custom plan: {kernel_name}")
+
+
+def run_planned_kernel(kernel_name, plan, rowptr, colind, vals, B):
+    """ra_real_graph_eval.py:266-285."""
+    if kernel_name == "CSR_DIRECT":
+        return _C.spmm_csr_direct(rowptr, colind, vals, B)
+    if kernel_name == "CSR_BASELINE":
+        return _C.spmm_csr_baseline(rowptr, colind, vals, B)
+    if kernel_name == "ZERO_OVERHEAD_CSR":
+        return _C.run_zero_overhead_plan(plan, rowptr, colind, vals, B)
+    if kernel_name == "TC_DIRECT":
+        return _C.run_tc_direct_plan(plan, B)
+    if kernel_name == "TC_DIRECT_TF32":
+        return _C.run_tc_direct_plan_tf32(plan, B)
+    if kernel_name == "COMMUNITY_TC":
+        return _C.run_community_tc_plan(plan, B)
+    if kernel_name == "COMMUNITY_TC_TF32":
+        return _C.run_community_tc_plan_tf32(plan, B)
+    if kernel_name == "SEGMENT_HYBRID":
+        return _C.run_segment_hybrid_plan(plan, colind, vals, B)
+    if kernel_name == "SEGMENT_HYBRID_TF32":
+        return _C.run_segment_hybrid_plan_tf32(plan, colind, vals, B)
+    raise ValueError(f"Unknown planned kernel: {kernel_name}")
+
+
+def make_timing_breakdown(plan_ms: float, exec_ms: float, nnz: int, N: int) -> dict:
+    """bench/benchmark.cpp:29-37: GFLOP/s = 2*nnz*N / (exec_ms * 1e6)."""
+    gflops = (2.0 * nnz * N) / (exec_ms * 1e6) if exec_ms > 0 else 0.0
+    return {"plan_ms": plan_ms, "exec_ms": exec_ms, "total_ms": plan_ms + exec_ms,
+            "gflops": gflops}
+
+
+def measure_exec_ms(fn, warmup: int = 3, iters: int = 10) -> float:
+    """Warmup, then one event pair around `iters` calls; mean ms per call
+    (bench/benchmark.cpp:39-67)."""
+    if iters <= 0:
+        return 0.0
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def measure_one_ms(fn):
+    """One event-timed call; returns (output, ms) (ra_real_graph_eval.py:210-221)."""
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    out = fn()
+    stop.record()
+    stop.synchronize()
+    return out, start.elapsed_time(stop)
+
+
+def benchmark_cusparse(rowptr, colind, vals, B, warmup: int = 3, iters: int = 10) -> dict:
+    """Warm guardrail timing (baseline CSR kernel), bindings/ra_bindings.cpp:838-866."""
+    plan = _C.make_cusparse_plan(rowptr, colind, vals, B)
+    ms = measure_exec_ms(lambda: _C.run_cusparse_plan(plan, B), warmup, max(1, iters))
+    d = make_timing_breakdown(0.0, ms, int(colind.numel()), int(B.shape[1]))
+    d.update(path="CUSPARSE", in_main_portfolio=False, legacy_baseline=False,
+             external_baseline=True, cusparse_algorithm=plan.algorithm, preprocess_ms=0.0)
+    return d
+
+
+def benchmark_cusparse_cold(rowptr, colind, vals, B, iters: int = 10) -> dict:
+    """Cold guardrail timing: plan construction + one execution, averaged."""
+    plan_sum = exec_sum = 0.0
+    name = ""
+    for _ in range(max(1, iters)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plan = _C.make_cusparse_plan(rowptr, colind, vals, B)
+        torch.cuda.synchronize()
+        plan_sum += (time.perf_counter() - t0) * 1e3
+        _, ms = measure_one_ms(lambda: _C.run_cusparse_plan(plan, B))
+        exec_sum += ms
+        name = plan.algorithm
+    n = float(max(1, iters))
+    d = make_timing_breakdown(plan_sum / n, exec_sum / n, int(colind.numel()), int(B.shape[1]))
+    d.update(path="CUSPARSE", in_main_portfolio=True, legacy_baseline=False,
+             external_baseline=False, cusparse_algorithm=name, preprocess_ms=plan_sum / n)
+    return d
+
+
+def run_router_plan(plan_dict, rowptr, colind, vals, B):
+    """One-shot helper: builds the chosen plan and runs it once
+    (bindings/ra_bindings.cpp:1762-1881).  Not for warm timing."""
+    label = route_label(plan_dict)
+    M = int(rowptr.numel()) - 1
+    K, N = int(B.shape[0]), int(B.shape[1])
+    if label == "CUSPARSE":
+        return _C.spmm_cusparse(rowptr, colind, vals, B)
+    plan = build_kernel_plan(label, rowptr.cpu(), colind.cpu(), vals.cpu(), M, K, N)
+    return run_planned_kernel(label, plan, rowptr, colind, vals, B)
+
+
+def _router_generic(rowptr, colind, vals, B, portfolio, warmup, iters, cold, table="mi355x"):
+    M = int(rowptr.numel()) - 1
+    K, N = int(B.shape[0]), int(B.shape[1])
+    nnz = int(colind.numel())
+    t0 = time.perf_counter()
+    plan_dict = _C.make_router_plan(rowptr, colind, vals, M, K, N, portfolio, table)
+    route_ms = (time.perf_counter() - t0) * 1e3
+    label = route_label(plan_dict)
+    if label == "CUSPARSE":
+        t1 = time.perf_counter()
+        p = _C.make_cusparse_plan(rowptr, colind, vals, B)
+        build_ms = (time.perf_counter() - t1) * 1e3
+        fn = lambda: _C.run_cusparse_plan(p, B)  # noqa: E731
+    else:
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        p = build_kernel_plan(label, rowptr.cpu(), colind.cpu(), vals.cpu(), M, K, N)
+        torch.cuda.synchronize()
+        build_ms = (time.perf_counter() - t1) * 1e3
+        fn = lambda: run_planned_kernel(label, p, rowptr, colind, vals, B)  # noqa: E731
+    if cold:
+        _, exec_ms = measure_one_ms(fn)
+        d = make_timing_breakdown(route_ms + build_ms, exec_ms, nnz, N)
+    else:
+        d = make_timing_breakdown(0.0, measure_exec_ms(fn, warmup, iters), nnz, N)
+    d.update(path=label, route_ms=route_ms, preprocess_ms=build_ms, router_plan=plan_dict)
+    return d
+
+
+def run_router_warm(rowptr, colind, vals, B, portfolio="MAIN", warmup=3, iters=10, table="mi355x"):
+    return _router_generic(rowptr, colind, vals, B, portfolio, warmup, iters, False, table)
+
+
+def run_router_cold(rowptr, colind, vals, B, portfolio="MAIN", warmup=3, iters=10, table="mi355x"):
+    return _router_generic(rowptr, colind, vals, B, portfolio, warmup, iters, True, table)
+
+
+def _oracle_generic(rowptr, colind, vals, B, warmup, iters, cold, kernels=None):
+    """Time every deployed path; report the fastest (the routing oracle)."""
+    M = int(rowptr.numel()) - 1
+    K, N = int(B.shape[0]), int(B.shape[1])
+    nnz = int(colind.numel())
+    kernels = kernels or DEPLOYED_KERNELS
+    results = {}
+    for k in kernels:
+        if k in TILE_KERNELS and N < 16:
+            continue
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        p = build_kernel_plan(k, rowptr.cpu(), colind.cpu(), vals.cpu(), M, K, N)
+        torch.cuda.synchronize()
+        build_ms = (time.perf_counter() - t0) * 1e3
+        fn = lambda: run_planned_kernel(k, p, rowptr, colind, vals, B)  # noqa: E731
+        if cold:
+            _, ms = measure_one_ms(fn)
+            results[k] = make_timing_breakdown(build_ms, ms, nnz, N)
+        else:
+            results[k] = make_timing_breakdown(0.0, measure_exec_ms(fn, warmup, iters), nnz, N)
+        del p
+    key = "total_ms" if cold else "exec_ms"
+    best = min(results, key=lambda k: results[k][key])
+    d = dict(results[best])
+    d.update(path=best, per_path=results)
+    return d
+
+
+def run_oracle_warm(rowptr, colind, vals, B, warmup=3, iters=10, portfolio="MAIN"):
+    return _oracle_generic(rowptr, colind, vals, B, warmup, iters, False)
+
+
+def run_oracle_cold(rowptr, colind, vals, B, warmup=3, iters=10, portfolio="MAIN"):
+    return _oracle_generic(rowptr, colind, vals, B, warmup, iters, True)
+
+
+def gpu_info_next() -> dict:
+    """Device properties of the current GPU."""
+    p = torch.cuda.get_device_properties(torch.cuda.current_device())
+    return {"name": p.name, "gcn_arch": getattr(p, "gcnArchName", ""),
+            "multi_processor_count": p.multi_processor_count,
+            "total_memory": p.total_memory, "backend": "hip"}

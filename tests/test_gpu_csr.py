@@ -1,0 +1,168 @@
+"""GPU parity of the CSR family (CSR_DIRECT, baseline, ZERO_OVERHEAD_CSR) and
+the GPU feature pass, against the oracle.
+
+Bar: CSR_DIRECT, the baseline kernel and the short-row bins (<= 64 nnz) of
+ZERO_OVERHEAD_CSR are bit-identical to oracle.spmm_seq_f32 (same fma chain per
+element).  Rows longer than 64 nnz go through 256-nnz chunks whose parts are
+summed in a fixed order: within 1e-5 of |A||B| (elementwise) of the fp64
+value, and bit-identical from run to run.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_scaled
+
+pytestmark = pytest.mark.gpu
+
+import ra_spmm  # noqa: E402
+from ra_spmm import synthetic as S  # noqa: E402
+from ra_spmm import capi  # noqa: E402
+
+
+def _dev(g):
+    return g.torch("cuda")
+
+
+def _B(K, N, seed):
+    return np.random.default_rng(seed).standard_normal((K, N)).astype(np.float32)
+
+
+CASES = [
+    # (M, K, avg_deg, skew, empty_frac, N)
+    (257, 300, 5.0, 0.0, 0.1, 16),
+    (1000, 800, 9.0, 1.3, 0.05, 32),
+    (1000, 1000, 12.0, 1.1, 0.0, 47),     # ragged N: scalar packets
+    (2048, 1500, 20.0, 1.2, 0.02, 64),
+    (3000, 2000, 16.0, 1.05, 0.01, 128),
+    (1500, 1500, 30.0, 1.5, 0.0, 256),
+    (700, 900, 25.0, 1.5, 0.0, 512),
+    (300, 400, 10.0, 1.0, 0.0, 1000),     # multi-tile columns
+    (5, 5, 0.0, 0.0, 0.0, 64),            # all rows empty
+]
+
+
+@pytest.mark.parametrize("M,K,d,skew,empty,N", CASES)
+def test_csr_direct_and_baseline_bit_exact(oracle, M, K, d, skew, empty, N):
+    print(f"[csr] M={M} K={K} d={d} N={N}", flush=True)
+    g = S.random_csr(M, K, d, seed=M + N, skew=skew, empty_frac=empty)
+    B = _B(K, N, seed=N)
+    ref = oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
+    rp, ci, vl = _dev(g)
+    Bd = torch.from_numpy(B).cuda()
+    for fn in (ra_spmm.spmm_csr_direct, ra_spmm.spmm_csr_baseline, ra_spmm.spmm_cusparse):
+        C = fn(rp, ci, vl, Bd)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(C.cpu().numpy(), ref, err_msg=fn.__name__)
+
+
+def test_csr_direct_unaligned_B_uses_scalar_path(oracle):
+    g = S.random_csr(500, 400, 8.0, seed=9)
+    B = _B(400, 65, seed=3)
+    big = torch.from_numpy(B).cuda().reshape(-1)
+    # A view starting 4 bytes in: not 16-byte aligned, contiguous.
+    storage = torch.zeros(big.numel() + 1, device="cuda")
+    storage[1:] = big
+    Bu = storage[1:].view(400, 65)
+    rp, ci, vl = _dev(g)
+    C = ra_spmm.spmm_csr_direct(rp, ci, vl, Bu)
+    np.testing.assert_array_equal(C.cpu().numpy(), oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B))
+
+
+@pytest.mark.parametrize("N", [32, 47, 64, 128, 256, 512])
+def test_zero_overhead_hub_rows(oracle, N):
+    print(f"[zo] N={N}", flush=True)
+    # Power-law rows: tiny/short/medium/long bins plus multi-chunk hubs.
+    g = S.random_csr(3000, 4000, 10.0, seed=N, skew=0.9, empty_frac=0.03, max_deg=3000)
+    deg = np.diff(g.rowptr)
+    assert deg.max() > 256 and (deg == 0).any()
+    B = _B(4000, N, seed=N + 1)
+    rp, ci, vl = _dev(g)
+    plan = ra_spmm.make_zero_overhead_plan(rp.cpu(), 3000, 4000)
+    bins = oracle.zo_bins(g.rowptr)
+    assert (plan.num_tiny, plan.num_short, plan.num_medium, plan.num_long, plan.num_empty) == (
+        bins["num_tiny"], bins["num_short"], bins["num_medium"], bins["num_long"], bins["num_empty"])
+    C = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, torch.from_numpy(B).cuda()).cpu().numpy()
+    seq = oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
+    short = deg <= 64
+    np.testing.assert_array_equal(C[short], seq[short])
+    c64 = oracle.spmm_f64(g.rowptr, g.colind, g.vals, B)
+    scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B))
+    assert_close_scaled(C, c64, scale, 1e-5, "zero_overhead")
+    # Deterministic: a second run is bit-identical.
+    C2 = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, torch.from_numpy(B).cuda()).cpu().numpy()
+    np.testing.assert_array_equal(C, C2)
+
+
+def test_features_device_equals_host():
+    for seed, (M, d, skew) in enumerate([(1, 3.0, 0), (1000, 5.0, 1.0), (200_003, 12.0, 1.1)]):
+        g = S.random_csr(M, 5000, d, seed=seed, skew=skew, empty_frac=0.01)
+        rp = torch.from_numpy(g.rowptr)
+        fd = ra_spmm.compute_features(rp.cuda(), M, 5000, 64)
+        fh = ra_spmm.compute_features(rp, M, 5000, 64)
+        for k in ("nnz", "sum_deg_sq", "max_deg", "empty_rows", "avg_nnz_per_row", "degree_cv"):
+            assert fd[k] == fh[k], k
+        py = ra_spmm.production_features(g.rowptr)
+        assert fd["avg_nnz_per_row"] == py["avg_nnz_per_row"]
+        assert fd["degree_cv"] == py["degree_cv"]
+
+
+def test_router_plan_device_equals_host():
+    g = S.random_csr(20_000, 20_000, 9.0, seed=4, skew=1.3)
+    rp = torch.from_numpy(g.rowptr)
+    for N in (16, 64, 128, 512):
+        a = ra_spmm.make_router_plan(rp.cuda(), rp, rp, g.M, g.K, N)
+        b = ra_spmm.make_router_plan(rp, rp, rp, g.M, g.K, N)
+        assert a["feature_backend"] == "cuda_rowptr_moments"
+        assert (a["chosen_path"], a["use_tf32"]) == (b["chosen_path"], b["use_tf32"])
+
+
+def test_capi_csr_direct_direct_call(oracle):
+    """The C ABI called directly (ctypes, no torch binding) on torch buffers."""
+    lib = capi.load()
+    g = S.random_csr(800, 700, 11.0, seed=21, skew=1.2)
+    B = _B(700, 128, seed=5)
+    rp, ci, vl = _dev(g)
+    Bd = torch.from_numpy(B).cuda()
+    C = torch.empty(800, 128, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    capi.check(lib.ra_spmm_csr_direct(capi.ptr(rp), capi.ptr(ci), capi.ptr(vl), capi.ptr(Bd),
+                                      capi.ptr(C), 800, 700, 128, g.nnz, stream))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(C.cpu().numpy(), oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B))
+
+
+def test_c2_full_size_properties(oracle):
+    """BASELINE config 2 at full size: bit-exact against the oracle on a row
+    sample, linearity in B and the all-ones row-sum identity on every row."""
+    g = S.CONFIGS["C2"]()
+    rp, ci, vl = _dev(g)
+    N = 128
+    rng = np.random.default_rng(12)
+    B = torch.from_numpy(rng.standard_normal((g.K, N)).astype(np.float32)).cuda()
+    plan = ra_spmm.make_zero_overhead_plan(rp.cpu(), g.M, g.K)
+    C_zo = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, B)
+    C_cd = ra_spmm.spmm_csr_direct(rp, ci, vl, B)
+    deg = np.diff(g.rowptr)
+    sample = np.concatenate([np.arange(0, g.M, 997), np.argsort(deg)[-50:]])
+    Bn = B.cpu().numpy()
+    for rows in (sample,):
+        sub_rp = np.concatenate([[0], np.cumsum(deg[rows])]).astype(np.int32)
+        sub_ci = np.concatenate([g.colind[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+        sub_vl = np.concatenate([g.vals[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+        seq = oracle.spmm_seq_f32(sub_rp, sub_ci, sub_vl, Bn)
+        np.testing.assert_array_equal(C_cd.cpu().numpy()[rows], seq)
+        c64 = oracle.spmm_f64(sub_rp, sub_ci, sub_vl, Bn)
+        scale = oracle.spmm_f64(sub_rp, sub_ci, np.abs(sub_vl), np.abs(Bn))
+        assert_close_scaled(C_zo.cpu().numpy()[rows], c64, scale, 1e-5, "C2 zero_overhead")
+    ones = torch.ones(g.K, 4, device="cuda")
+    rs = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, ones)[:, 0].double().cpu().numpy()
+    exact = np.add.reduceat(np.append(g.vals.astype(np.float64), 0), g.rowptr[:-1])
+    exact[deg == 0] = 0
+    assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1.0, np.abs(exact)))
+    # Linearity: A(2B + B') == 2AB + AB' within fp32 rounding.
+    B2 = torch.randn(g.K, N, device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    lhs = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, 2 * B + B2)
+    rhs = 2 * C_zo + ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, B2)
+    sc = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl.abs(), (2 * B).abs() + B2.abs())
+    assert torch.all((lhs - rhs).abs() <= 1e-5 * sc + 1e-30)
