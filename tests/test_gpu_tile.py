@@ -1,0 +1,143 @@
+"""GPU parity of the tile family (TC_DIRECT, COMMUNITY_TC, SEGMENT_HYBRID).
+
+Stated tolerances (elementwise, scaled by |A||B| so cancellation cannot
+inflate them):
+  FP16 MFMA route   vs fp64 of the fp16-quantised inputs: 1e-5 (fp16 x fp16
+                    products are exact in fp32; only summation order differs);
+                    vs fp64 of the unquantised inputs: 2^-10 (two fp16
+                    roundings of 2^-11 each).
+  BF16 MFMA route   vs fp64 of the bf16-quantised inputs: 1e-5; unquantised: 2^-7.
+  FP32-FMA route    (replaces the reference TF32 path) TC_DIRECT/COMMUNITY_TC:
+                    bit-identical to the sequential fp32 fma chain over the
+                    fp16-stored values in column order; SEGMENT_HYBRID split
+                    windows: 1e-5.
+The reference's own gate is 1e-2 * sqrt(max row nnz) absolute for tile paths
+(ra_real_graph_eval.py:41-51, 478-495); every bound above is tighter.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_scaled
+
+pytestmark = pytest.mark.gpu
+
+import ra_spmm  # noqa: E402
+from ra_spmm import synthetic as S  # noqa: E402
+
+MAKE = {0: ra_spmm.make_tc_direct_plan, 1: ra_spmm.make_community_tc_plan,
+        2: ra_spmm.make_segment_hybrid_plan}
+
+
+def run(kind, plan, B, route, g_dev):
+    rp, ci, vl = g_dev
+    if kind == 0:
+        return (ra_spmm.run_tc_direct_plan_tf32 if route == "fp32" else ra_spmm.run_tc_direct_plan)(plan, B)
+    if kind == 1:
+        return (ra_spmm.run_community_tc_plan_tf32 if route == "fp32" else ra_spmm.run_community_tc_plan)(plan, B)
+    fn = ra_spmm.run_segment_hybrid_plan_tf32 if route == "fp32" else ra_spmm.run_segment_hybrid_plan
+    return fn(plan, ci, vl, B)
+
+
+GRAPHS = {
+    "skewed": lambda: S.random_csr(1003, 900, 9.0, seed=3, skew=1.1, empty_frac=0.05),
+    "dense_rows": lambda: S.random_csr(200, 3000, 150.0, seed=4),    # > 64 blocks per window
+    "community": lambda: S.sbm(64, 50, 12.0, 0.9, seed=6),
+}
+
+
+@pytest.mark.parametrize("gname", list(GRAPHS))
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("N", [16, 32, 47, 64, 128, 256, 512])
+def test_tile_routes(oracle, gname, kind, N):
+    print(f"[tile] {gname} kind={kind} N={N}", flush=True)
+    g = GRAPHS[gname]()
+    gd = g.torch("cuda")
+    B = np.random.default_rng(N + kind).standard_normal((g.K, N)).astype(np.float32)
+    Bd = torch.from_numpy(B).cuda()
+    exact = oracle.spmm_f64(g.rowptr, g.colind, g.vals, B)
+    scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B))
+
+    plan = MAKE[kind](gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, N)
+    assert plan.valid and plan.active
+    C = run(kind, plan, Bd, "f16", gd).cpu().numpy()
+    qv, qb = oracle.quantize_f16(g.vals), oracle.quantize_f16(B)
+    assert_close_scaled(C, oracle.spmm_tile_f64(g.rowptr, g.colind, g.vals, B, "f16"),
+                        oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5, "f16 vs quantised")
+    assert_close_scaled(C, exact, scale, 2.0 ** -10, "f16 vs exact")
+
+    C32 = run(kind, plan, Bd, "fp32", gd).cpu().numpy()
+    seq = oracle.spmm_seq_f32(g.rowptr, g.colind, qv, B)
+    if kind == 2 and plan.num_split_windows > 0:
+        assert_close_scaled(C32, oracle.spmm_f64(g.rowptr, g.colind, qv, B),
+                            oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(B)), 1e-5, "fp32 seg")
+    else:
+        np.testing.assert_array_equal(C32, seq)
+
+    # Deterministic across runs.
+    np.testing.assert_array_equal(run(kind, plan, Bd, "f16", gd).cpu().numpy(), C)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_bf16_plan_and_lowp_entry(oracle, kind):
+    g = GRAPHS["skewed"]()
+    gd = g.torch("cuda")
+    N = 128
+    B = np.random.default_rng(9).standard_normal((g.K, N)).astype(np.float32)
+    Bd = torch.from_numpy(B).cuda()
+    plan = MAKE[kind](gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, N, "bf16")
+    C = run(kind, plan, Bd, "bf16", gd).cpu().numpy()
+    qv, qb = oracle.quantize_bf16(g.vals), oracle.quantize_bf16(B)
+    assert_close_scaled(C, oracle.spmm_tile_f64(g.rowptr, g.colind, g.vals, B, "bf16"),
+                        oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5, "bf16")
+    assert_close_scaled(C, oracle.spmm_f64(g.rowptr, g.colind, g.vals, B),
+                        oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B)), 2.0 ** -7, "bf16 exact")
+    # Native bf16 B: no conversion pass, identical result.
+    C2 = run(kind, plan, Bd.to(torch.bfloat16), "bf16", gd).cpu().numpy()
+    np.testing.assert_array_equal(C, C2)
+    # fp16 plan with native fp16 B.
+    p16 = MAKE[kind](gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, N)
+    np.testing.assert_array_equal(run(kind, p16, Bd, "f16", gd).cpu().numpy(),
+                                  run(kind, p16, Bd.half(), "f16", gd).cpu().numpy())
+
+
+def test_inactive_plan_raises_and_families_agree(oracle):
+    g = GRAPHS["community"]()
+    gd = g.torch("cuda")
+    p = ra_spmm.make_tc_direct_plan(gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, 8)
+    assert not p.active
+    with pytest.raises(RuntimeError):
+        ra_spmm.run_tc_direct_plan(p, torch.randn(g.K, 64, device="cuda"))
+    B = torch.randn(g.K, 64, device="cuda")
+    outs = [run(k, MAKE[k](gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, 64), B, "fp32", gd)
+            for k in (0, 1, 2)]
+    np.testing.assert_array_equal(outs[0].cpu().numpy(), outs[1].cpu().numpy())
+    torch.testing.assert_close(outs[0], outs[2], rtol=1e-5, atol=1e-6)
+
+
+def test_c3_full_size_properties(oracle):
+    """BASELINE config 3 (SBM, fp16 values) at full size through TC_DIRECT and
+    COMMUNITY_TC: a row sample against the oracle, and all-ones row sums."""
+    g = S.CONFIGS["C3"]()
+    gd = g.torch("cuda")
+    N = 256
+    rng = np.random.default_rng(2)
+    B = rng.standard_normal((g.K, N)).astype(np.float16).astype(np.float32)
+    Bd = torch.from_numpy(B).cuda()
+    deg = np.diff(g.rowptr)
+    rows = np.arange(0, g.M, 1021)
+    sub_rp = np.concatenate([[0], np.cumsum(deg[rows])]).astype(np.int32)
+    sub_ci = np.concatenate([g.colind[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    sub_vl = np.concatenate([g.vals[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    ref = oracle.spmm_f64(sub_rp, sub_ci, sub_vl, B)
+    scale = oracle.spmm_f64(sub_rp, sub_ci, np.abs(sub_vl), np.abs(B))
+    for kind in (0, 1, 2):
+        plan = MAKE[kind](gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, N)
+        C = run(kind, plan, Bd, "f16", gd)
+        assert_close_scaled(C.cpu().numpy()[rows], ref, scale, 1e-5, f"C3 kind {kind}")
+        ones = torch.ones(g.K, 16, device="cuda")
+        rs = run(kind, plan, ones, "f16", gd)[:, 0].double().cpu().numpy()
+        exact = np.add.reduceat(np.append(g.vals.astype(np.float64), 0), g.rowptr[:-1])
+        exact[deg == 0] = 0
+        assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
+        del plan

@@ -1,0 +1,155 @@
+"""Host plan builders of the product against the oracle restatements.
+
+ZERO_OVERHEAD_CSR binning (csr/ra_zero_overhead.cu:331-358) and the tile
+format of the three tile families (tc/ra_tc_direct.cu:654-706,
+tc/ra_community_tc.cu:335-403, tc/ra_segment_hybrid.cu:470-498) are compared
+array by array; the oracle tile format itself is pinned by decode == CSR and
+its counting invariants; fp16/bf16 value rounding is checked against numpy.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import torch  # noqa: F401
+from ra_spmm import capi
+from ra_spmm import synthetic as S
+
+
+def zo_bins_capi(rowptr, M, K):
+    lib = capi.load()
+    info = capi.ZOInfo()
+    capi.check(lib.ra_zo_bins_host(capi.ptr(rowptr), M, K, None, None, None, None, ctypes.byref(info)))
+    small = np.zeros(max(1, info.num_small), np.int32)
+    crow = np.zeros(max(1, info.num_chunks), np.int32)
+    cst = np.zeros(max(1, info.num_chunks), np.int32)
+    emp = np.zeros(max(1, info.num_empty), np.int32)
+    capi.check(lib.ra_zo_bins_host(capi.ptr(rowptr), M, K, capi.ptr(small), capi.ptr(crow),
+                                   capi.ptr(cst), capi.ptr(emp), ctypes.byref(info)))
+    return info, small[:info.num_small], crow[:info.num_chunks], cst[:info.num_chunks], emp[:info.num_empty]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_zo_bins_match_oracle(oracle, seed):
+    g = S.random_csr(4000, 5000, 12.0, seed=seed, skew=0.9, empty_frac=0.05, max_deg=2000)
+    info, small, crow, cst, emp = zo_bins_capi(g.rowptr, g.M, g.K)
+    o = oracle.zo_bins(g.rowptr)
+    np.testing.assert_array_equal(small, o["small_rows"])
+    np.testing.assert_array_equal(crow.view(np.uint32).astype(np.int64), o["chunk_rows"])
+    np.testing.assert_array_equal(cst, o["chunk_starts"])
+    assert (info.num_tiny, info.num_short, info.num_medium, info.num_long, info.num_empty,
+            info.max_long_chunks) == (o["num_tiny"], o["num_short"], o["num_medium"],
+                                      o["num_long"], o["num_empty"], o["max_long_chunks"])
+    # Brute-force invariants: every nonzero is covered exactly once.
+    deg = np.diff(g.rowptr)
+    covered = np.zeros(g.nnz, np.int32)
+    for r in small:
+        covered[g.rowptr[r]:g.rowptr[r + 1]] += 1
+    for t, s in zip(crow.view(np.uint32), cst):
+        row = int(t & 0x7FFFFFFF)
+        covered[s:min(s + 256, g.rowptr[row + 1])] += 1
+        assert bool(t & 0x80000000) == (deg[row] <= 256)
+    assert np.all(covered == 1)
+    assert set(emp.tolist()) == set(np.flatnonzero(deg == 0).tolist())
+
+
+def tile_host(kind, g, N=64, value_dtype=capi.DTYPE_F16):
+    lib = capi.load()
+    h = ctypes.c_void_p()
+    capi.check(lib.ra_tile_host_build(kind, capi.ptr(g.rowptr), capi.ptr(g.colind), capi.ptr(g.vals),
+                                      g.M, g.K, N, value_dtype, ctypes.byref(h)))
+    info = capi.TileInfo()
+    capi.check(lib.ra_tile_host_get_info(h, ctypes.byref(info)))
+    out = {}
+    for name in ("block_offsets", "atox", "win_rows", "vals", "seg_window", "seg_bbegin",
+                 "seg_bend", "seg_slot", "split_windows", "split_offsets"):
+        n = ctypes.c_int64()
+        capi.check(lib.ra_tile_host_export(h, name.encode(), None, ctypes.byref(n)))
+        arr = np.zeros(n.value, np.uint16 if name == "vals" else np.int32)
+        if n.value:
+            capi.check(lib.ra_tile_host_export(h, name.encode(), capi.ptr(arr), ctypes.byref(n)))
+        out[name] = arr
+    lib.ra_tile_host_destroy(h)
+    return info, out
+
+
+def _graphs():
+    yield S.random_csr(203, 180, 6.0, seed=1, skew=1.2, empty_frac=0.1)
+    yield S.random_csr(64, 400, 90.0, seed=2)          # windows with > 64 blocks
+    yield S.sbm(8, 40, 10.0, 0.9, seed=5)               # community structure
+    yield S.random_csr(9, 9, 0.0, seed=3)               # empty matrix
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_tile_format_matches_oracle(oracle, kind):
+    for g in _graphs():
+        info, h = tile_host(kind, g)
+        o = oracle.tile_format(kind, g.rowptr, g.colind, g.vals, g.M)
+        W = (g.M + 7) // 8
+        assert info.active == 1 and info.num_windows == W
+        np.testing.assert_array_equal(h["win_rows"], o["win_rows"])
+        np.testing.assert_array_equal(h["block_offsets"], o["block_offsets"])
+        real = h["atox"] >= 0
+        np.testing.assert_array_equal(h["atox"][real], o["atox"][real])
+        assert np.all(o["atox"][~real] == 0)  # reference pads with column 0
+        assert info.num_blocks == o["block_offsets"][-1]
+        assert info.num_vectors == int(real.sum())
+        vals = h["vals"].view(np.float16).astype(np.float32).reshape(-1, 8, 8)
+        np.testing.assert_array_equal(vals, oracle.quantize_f16(o["blocks"]))
+        if kind == 2:
+            for key in ("seg_bbegin", "seg_bend", "seg_slot", "split_windows", "split_offsets"):
+                np.testing.assert_array_equal(h[key], o[key], err_msg=key)
+            np.testing.assert_array_equal(h["seg_window"].view(np.uint32), o["seg_window"])
+
+
+def test_oracle_tile_format_invariants(oracle):
+    for kind in (0, 1, 2):
+        for g in _graphs():
+            o = oracle.tile_format(kind, g.rowptr, g.colind, g.vals, g.M)
+            dense = np.zeros((g.M, g.K))
+            for r in range(g.M):
+                for p in range(g.rowptr[r], g.rowptr[r + 1]):
+                    dense[r, g.colind[p]] += g.vals[p]
+            np.testing.assert_allclose(oracle.tile_decode(o, g.M, g.K), dense, rtol=1e-6)
+            bo = o["block_offsets"]
+            for w in range(len(bo) - 1):
+                rows = [int(r) for r in o["win_rows"][w * 8:(w + 1) * 8] if r >= 0]
+                cols = set()
+                for r in rows:
+                    cols.update(g.colind[g.rowptr[r]:g.rowptr[r + 1]].tolist())
+                assert bo[w + 1] - bo[w] == (len(cols) + 7) // 8
+            if kind == 1:
+                lead = [g.colind[g.rowptr[r]] if g.rowptr[r] < g.rowptr[r + 1] else 2**31 - 1
+                        for r in range(g.M)]
+                order = o["win_rows"][:g.M]
+                keys = [(lead[r], r) for r in order]
+                assert keys == sorted(keys)
+            if kind == 2:
+                nseg = sum(((bo[w + 1] - bo[w]) + 63) // 64 if bo[w + 1] - bo[w] > 64 else 1
+                           for w in range(len(bo) - 1))
+                assert len(o["seg_window"]) == nseg
+
+
+def test_value_rounding_matches_numpy(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 3000),
+                        np.array([65504, 65519.99, 65520, 2**-24, 2**-25, 1.5 * 2**-25, 2**-14,
+                                  2**-14 * (1 - 2**-11), -0.0, 0.0], np.float32)]).astype(np.float32)
+    x = x[np.abs(x) < 1e30]
+    M = len(x)
+    g = S.Graph(np.arange(M + 1, dtype=np.int32), np.zeros(M, np.int32), x, M, 1)
+    for vd, q in ((capi.DTYPE_F16, oracle.quantize_f16), (capi.DTYPE_BF16, oracle.quantize_bf16)):
+        _, h = tile_host(0, g, value_dtype=vd)
+        blocks = h["vals"].reshape(-1, 8, 8)[:, :, 0].reshape(-1)[:M]
+        if vd == capi.DTYPE_F16:
+            got = blocks.view(np.float16).astype(np.float32)
+        else:
+            got = (blocks.astype(np.uint32) << 16).view(np.float32)
+        with np.errstate(over="ignore"):
+            np.testing.assert_array_equal(got, q(x))
+
+
+def test_inactive_below_n16():
+    g = S.random_csr(20, 20, 3.0, seed=0)
+    info, _ = tile_host(0, g, N=8)
+    assert info.active == 0
