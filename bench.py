@@ -124,7 +124,20 @@ def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
     return ev, name
 
 
-def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10):
+def copy_probe(nbytes=1 << 30):
+    """One device-to-device copy of a known size: the reference point that
+    scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    import torch
+    src = torch.ones(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy probe: {nbytes} bytes read + {nbytes} bytes written")
+    del src, dst
+
+
+def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=None):
     import numpy as np
     import torch
     import ra_spmm
@@ -145,7 +158,7 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10):
         t = time.perf_counter()
         plan_dict = ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N, "MAIN", table)
         route_ms.append((time.perf_counter() - t) * 1e3)
-    label = ra_spmm.route_label(plan_dict)
+    label = force_path or ra_spmm.route_label(plan_dict)
     log(f"[bench] routed to {label} ({plan_dict['decision_reason']}), "
         f"d={plan_dict['feature_values']['avg_nnz_per_row']:.3f} "
         f"cv={plan_dict['feature_values']['degree_cv']:.3f}")
@@ -254,6 +267,8 @@ def main(argv=None):
     ap.add_argument("--sweep-N", default="64,128,256")
     ap.add_argument("--sweep-out", default="gpurun_out/sweep.json")
     ap.add_argument("--details", default=None, help="write the full result dict here")
+    ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
+    ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -270,7 +285,10 @@ def main(argv=None):
               args.sweep_out)
         return 0
 
-    res = bench_config(args.config, args.N, args.steps, args.warmup, args.table, not args.no_cpu)
+    if args.copy_probe:
+        copy_probe()
+    res = bench_config(args.config, args.N, args.steps, args.warmup, args.table, not args.no_cpu,
+                       force_path=args.path)
     achieved = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9
     line = {
         "metric": METRIC, "value": round(res["gflops"], 3), "unit": "GFLOP/s", "n_gpus": 1,

@@ -19,6 +19,7 @@
 // one fp32 accumulator updated by fma in CSR order, which is bit-identical to
 // the reference per-lane accumulation (csr/csr_direct.cu:201-228).
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 #include "ra_internal.hpp"
@@ -48,23 +49,40 @@ __device__ __forceinline__ float4 padd(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
+// Streaming (non-temporal) accesses for data touched once: the CSR index and
+// value streams and the C rows.  They then do not displace B rows that other
+// waves are about to gather again from L2.
+typedef float f32x4n __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ T load_once(const T* p, bool nt) {
+    return nt ? __builtin_nontemporal_load(p) : *p;
+}
+__device__ __forceinline__ void store_once(float* p, float v, bool nt) {
+    if (nt) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+__device__ __forceinline__ void store_once(float4* p, float4 v, bool nt) {
+    if (nt) __builtin_nontemporal_store(f32x4n{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4n*>(p));
+    else *p = v;
+}
+
 // Accumulate the nnz range [p0, p1) of one row into acc.  All G lanes of the
 // group share the range; lane `sl` owns packet columns q[s] (q < 0: masked).
 // Per output element the update order is p ascending, one fma per nonzero.
-template <int G, int V, typename P>
+template <int G, int V, int U, typename P>
 __device__ __forceinline__ void accumulate_range(const int32_t* __restrict__ colind,
                                                  const float* __restrict__ vals,
                                                  const P* __restrict__ Bp, int64_t ldp,
                                                  int p0, int p1, int sl, const int (&q)[V],
-                                                 P (&acc)[V]) {
-    constexpr int U = (G >= 4) ? 4 : G;  // gathers in flight per lane
+                                                 P (&acc)[V], bool nt) {
+    static_assert(U <= G, "unroll deeper than the lane group");
     for (int base = p0; base < p1; base += G) {
         const int my = base + sl;
         int mc = 0;
         float mv = 0.f;
         if (my < p1) {
-            mc = colind[my];
-            mv = vals[my];
+            mc = load_once(colind + my, nt);
+            mv = load_once(vals + my, nt);
         }
         const int cnt = min(G, p1 - base);
         for (int j = 0; j < cnt; j += U) {
@@ -95,18 +113,30 @@ __device__ __forceinline__ void accumulate_range(const int32_t* __restrict__ col
     }
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
+// With remap on, XCD x runs a contiguous range of logical blocks, so rows that
+// are close in the row order (and tend to share columns) share one L2.
+__device__ __forceinline__ int64_t logical_block(bool remap) {
+    const int64_t bid = blockIdx.x;
+    if (!remap) return bid;
+    const int64_t nb = gridDim.x, q = nb / 8, r = nb % 8;
+    const int64_t x = bid % 8, k = bid / 8;
+    return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
 // ---------------------------------------------------------------- CSR_DIRECT
-template <int G, int V, typename P>
+template <int G, int V, int U, typename P>
 __global__ __launch_bounds__(kBlock) void csr_rows_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
     const float* __restrict__ vals, const P* __restrict__ Bp, P* __restrict__ Cp,
-    const int32_t* __restrict__ row_list, int64_t num_rows, int64_t ldp, int np) {
+    const int32_t* __restrict__ row_list, int64_t num_rows, int64_t ldp, int np, int remap,
+    int nt) {
     constexpr int RPW = kWave / G;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int sub = lane / G;
     const int sl = lane % G;
-    const int64_t idx = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * RPW + sub;
+    const int64_t idx = (logical_block(remap) * kWavesPerBlock + wave) * RPW + sub;
     if (idx >= num_rows) return;  // whole lane groups leave together
     const int row = row_list ? row_list[idx] : static_cast<int>(idx);
     const int q0 = blockIdx.y * (G * V);
@@ -119,10 +149,11 @@ __global__ __launch_bounds__(kBlock) void csr_rows_kernel(
     P acc[V];
 #pragma unroll
     for (int s = 0; s < V; ++s) acc[s] = pzero<P>();
-    accumulate_range<G, V, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc);
+    accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc,
+                                 nt != 0);
 #pragma unroll
     for (int s = 0; s < V; ++s)
-        if (q[s] >= 0) Cp[(int64_t)row * ldp + q[s]] = acc[s];
+        if (q[s] >= 0) store_once(Cp + (int64_t)row * ldp + q[s], acc[s], nt != 0);
 }
 
 // ----------------------------------------------------------------- baseline
@@ -158,20 +189,21 @@ __global__ __launch_bounds__(kBlock) void csr_baseline_kernel(
 // Waves [0, num_chunks) take one 256-nnz chunk each; the 64/G lane groups of
 // the wave split the chunk into contiguous parts and are summed in group order
 // through LDS.  Later waves take 64/G rows of the short-row list each.
-template <int G, int V, typename P>
+template <int G, int V, int U, typename P>
 __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
     const float* __restrict__ vals, const P* __restrict__ Bp, P* __restrict__ Cp,
     const int32_t* __restrict__ chunk_rows, const int32_t* __restrict__ chunk_starts,
     const int32_t* __restrict__ chunk_slot, int num_chunks, P* __restrict__ partials,
-    const int32_t* __restrict__ short_rows, int64_t num_short, int64_t ldp, int np) {
+    const int32_t* __restrict__ short_rows, int64_t num_short, int64_t ldp, int np, int remap,
+    int nt) {
     constexpr int RPW = kWave / G;
     __shared__ P red[kWavesPerBlock][(RPW > 1 ? RPW - 1 : 1) * G * V];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int sub = lane / G;
     const int sl = lane % G;
-    const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    const int64_t gw = logical_block(remap) * kWavesPerBlock + wave;
     const int q0 = blockIdx.y * (G * V);
     int q[V];
 #pragma unroll
@@ -191,7 +223,7 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
         constexpr int L = kChunk / RPW;
         const int a = min(cs + sub * L, ce);
         const int b = min(a + L, ce);
-        accumulate_range<G, V, P>(colind, vals, Bp, ldp, a, b, sl, q, acc);
+        accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, a, b, sl, q, acc, nt != 0);
         if constexpr (RPW > 1) {
             if (sub > 0) {
 #pragma unroll
@@ -214,17 +246,18 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
             P* dst = (tag & kSoleFlag) ? Cp + (int64_t)row * ldp : partials + (int64_t)slot * ldp;
 #pragma unroll
             for (int s = 0; s < V; ++s)
-                if (q[s] >= 0) dst[q[s]] = acc[s];
+                if (q[s] >= 0) store_once(dst + q[s], acc[s], nt != 0);
         }
         return;
     }
     const int64_t idx = (gw - num_chunks) * RPW + sub;
     if (idx >= num_short) return;
     const int row = short_rows[idx];
-    accumulate_range<G, V, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc);
+    accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc,
+                                 nt != 0);
 #pragma unroll
     for (int s = 0; s < V; ++s)
-        if (q[s] >= 0) Cp[(int64_t)row * ldp + q[s]] = acc[s];
+        if (q[s] >= 0) store_once(Cp + (int64_t)row * ldp + q[s], acc[s], nt != 0);
 }
 
 // Deterministic merge: C[row] = ((slot0 + slot1) + slot2) + ... per element.
@@ -341,63 +374,95 @@ MomentBuffers g_moment[64];
 
 // --------------------------------------------------------------- dispatch
 struct LaneShape {
-    int G, V;
+    int G, V, U;
 };
+
+// Tuning knobs, read once per process: RA_CSR_LANES forces the lane-group
+// width (4..64), RA_CSR_UNROLL the gathers in flight per lane (4 or 8),
+// RA_XCD_REMAP=0 turns the XCD-contiguous block order of CSR_DIRECT off
+// (RA_ZO_XCD_REMAP=1 turns it on for ZERO_OVERHEAD_CSR, where it piles the hub
+// chunks onto one XCD), RA_CSR_STREAMING=0 turns the non-temporal hints off.
+struct CsrTuning {
+    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1;
+    CsrTuning() {
+        if (const char* e = std::getenv("RA_CSR_LANES")) lanes = std::atoi(e);
+        if (const char* e = std::getenv("RA_CSR_UNROLL")) unroll = std::atoi(e) >= 8 ? 8 : 4;
+        if (const char* e = std::getenv("RA_XCD_REMAP")) remap = std::atoi(e) != 0;
+        if (const char* e = std::getenv("RA_ZO_XCD_REMAP")) zo_remap = std::atoi(e) != 0;
+        if (const char* e = std::getenv("RA_CSR_STREAMING")) nt = std::atoi(e) != 0;
+    }
+};
+const CsrTuning& tuning() {
+    static const CsrTuning t;
+    return t;
+}
 
 // Lane-group shape from the number of packets per row.
 LaneShape pick_shape(int np) {
-    if (np <= 4) return {4, 1};
-    if (np <= 8) return {8, 1};
-    if (np <= 16) return {16, 1};
-    if (np <= 32) return {32, 1};
-    if (np <= 64) return {64, 1};
-    if (np <= 128) return {64, 2};
-    return {64, 4};
+    const CsrTuning& t = tuning();
+    int G;
+    if (t.lanes >= 4 && t.lanes <= 64 && (t.lanes & (t.lanes - 1)) == 0) G = t.lanes;
+    else G = np <= 4 ? 4 : np <= 8 ? 8 : np <= 16 ? 16 : np <= 32 ? 32 : 64;
+    int V = (np + G - 1) / G;
+    V = V <= 1 ? 1 : V <= 2 ? 2 : 4;
+    const int U = std::min(G, t.unroll);
+    return {G, V, U};
 }
 
 template <typename P>
-ra_status launch_csr_rows(int G, int V, dim3 grid, hipStream_t st, const int32_t* rowptr,
+ra_status launch_csr_rows(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_t* rowptr,
                           const int32_t* colind, const float* vals, const P* B, P* C,
                           const int32_t* row_list, int64_t num_rows, int64_t ldp, int np) {
-#define RA_ROWS_CASE(g, v)                                                                  \
-    if (G == g && V == v) {                                                                 \
-        csr_rows_kernel<g, v, P><<<grid, kBlock, 0, st>>>(rowptr, colind, vals, B, C,       \
-                                                          row_list, num_rows, ldp, np);     \
+    const int remap = tuning().remap, nt = tuning().nt;
+#define RA_ROWS_CASE(g, v, u)                                                               \
+    if (sh.G == g && sh.V == v && sh.U == u) {                                              \
+        csr_rows_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(rowptr, colind, vals, B, C,    \
+                                                             row_list, num_rows, ldp, np,   \
+                                                             remap, nt);                    \
         RA_LAUNCH_CHECK("csr_rows_kernel");                                                 \
         return RA_OK;                                                                       \
     }
-    RA_ROWS_CASE(4, 1)
-    RA_ROWS_CASE(8, 1)
-    RA_ROWS_CASE(16, 1)
-    RA_ROWS_CASE(32, 1)
-    RA_ROWS_CASE(64, 1)
-    RA_ROWS_CASE(64, 2)
-    RA_ROWS_CASE(64, 4)
+#define RA_ROWS_G(g, u) RA_ROWS_CASE(g, 1, u) RA_ROWS_CASE(g, 2, u) RA_ROWS_CASE(g, 4, u)
+    RA_ROWS_G(4, 4)
+    RA_ROWS_G(8, 4)
+    RA_ROWS_G(8, 8)
+    RA_ROWS_G(16, 4)
+    RA_ROWS_G(16, 8)
+    RA_ROWS_G(32, 4)
+    RA_ROWS_G(32, 8)
+    RA_ROWS_G(64, 4)
+    RA_ROWS_G(64, 8)
+#undef RA_ROWS_G
 #undef RA_ROWS_CASE
     return ra::fail(RA_ERR_INTERNAL, "csr_rows: no lane shape");
 }
 
 template <typename P>
-ra_status launch_zo(int G, int V, dim3 grid, hipStream_t st, const int32_t* rowptr,
+ra_status launch_zo(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_t* rowptr,
                     const int32_t* colind, const float* vals, const P* B, P* C,
                     const int32_t* chunk_rows, const int32_t* chunk_starts,
                     const int32_t* chunk_slot, int num_chunks, P* partials,
                     const int32_t* short_rows, int64_t num_short, int64_t ldp, int np) {
-#define RA_ZO_CASE(g, v)                                                                     \
-    if (G == g && V == v) {                                                                  \
-        zo_fused_kernel<g, v, P><<<grid, kBlock, 0, st>>>(                                   \
+    const int remap = tuning().zo_remap, nt = tuning().nt;
+#define RA_ZO_CASE(g, v, u)                                                                  \
+    if (sh.G == g && sh.V == v && sh.U == u) {                                               \
+        zo_fused_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(                                \
             rowptr, colind, vals, B, C, chunk_rows, chunk_starts, chunk_slot, num_chunks,    \
-            partials, short_rows, num_short, ldp, np);                                       \
+            partials, short_rows, num_short, ldp, np, remap, nt);                            \
         RA_LAUNCH_CHECK("zo_fused_kernel");                                                  \
         return RA_OK;                                                                        \
     }
-    RA_ZO_CASE(4, 1)
-    RA_ZO_CASE(8, 1)
-    RA_ZO_CASE(16, 1)
-    RA_ZO_CASE(32, 1)
-    RA_ZO_CASE(64, 1)
-    RA_ZO_CASE(64, 2)
-    RA_ZO_CASE(64, 4)
+#define RA_ZO_G(g, u) RA_ZO_CASE(g, 1, u) RA_ZO_CASE(g, 2, u) RA_ZO_CASE(g, 4, u)
+    RA_ZO_G(4, 4)
+    RA_ZO_G(8, 4)
+    RA_ZO_G(8, 8)
+    RA_ZO_G(16, 4)
+    RA_ZO_G(16, 8)
+    RA_ZO_G(32, 4)
+    RA_ZO_G(32, 8)
+    RA_ZO_G(64, 4)
+    RA_ZO_G(64, 8)
+#undef RA_ZO_G
 #undef RA_ZO_CASE
     return ra::fail(RA_ERR_INTERNAL, "zo: no lane shape");
 }
@@ -440,10 +505,10 @@ ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
     const int rows_per_block = kWavesPerBlock * (kWave / sh.G);
     dim3 grid((M + rows_per_block - 1) / rows_per_block, (np + sh.G * sh.V - 1) / (sh.G * sh.V));
     if (vec)
-        return launch_csr_rows<float4>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals,
+        return launch_csr_rows<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
                                        reinterpret_cast<const float4*>(d_B),
                                        reinterpret_cast<float4*>(d_C), nullptr, M, np, np);
-    return launch_csr_rows<float>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
+    return launch_csr_rows<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
                                   nullptr, M, np, np);
 }
 
@@ -625,14 +690,14 @@ ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
         dim3 grid((waves + kWavesPerBlock - 1) / kWavesPerBlock, tiles);
         ra_status s;
         if (vec)
-            s = launch_zo<float4>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals,
+            s = launch_zo<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
                                   reinterpret_cast<const float4*>(d_B), reinterpret_cast<float4*>(d_C),
                                   plan->chunk_rows.get<int32_t>(), plan->chunk_starts.get<int32_t>(),
                                   plan->chunk_slot.get<int32_t>(), plan->info.num_chunks,
                                   plan->partials.get<float4>(), plan->short_rows.get<int32_t>(),
                                   plan->num_short_total, np, np);
         else
-            s = launch_zo<float>(sh.G, sh.V, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
+            s = launch_zo<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
                                  plan->chunk_rows.get<int32_t>(), plan->chunk_starts.get<int32_t>(),
                                  plan->chunk_slot.get<int32_t>(), plan->info.num_chunks,
                                  plan->partials.get<float>(), plan->short_rows.get<int32_t>(),
