@@ -213,6 +213,46 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
     return res
 
 
+def bench_gcn(steps, warmup, table, backends=("router", "cusparse", "zero_overhead", "csr_direct")):
+    """2-layer GCN training step (128 -> 256 -> 47) on the
+    synthetic power-law operator, forward A X and backward A^T G routed per
+    (transpose, N).  Reports step time per backend and the routed paths."""
+    import numpy as np
+    import scipy.sparse as sp
+    import torch
+    from ra_spmm import gnn
+    from ra_spmm import synthetic as S
+    g = S.CONFIGS["C5"]()
+    op = sp.csr_matrix((g.vals, g.colind, g.rowptr), shape=(g.M, g.M))
+    torch.manual_seed(0)
+    X = torch.randn(g.M, 128, device="cuda")
+    y = torch.randint(0, 47, (g.M,), device="cuda")
+    out = {"graph": g.name, "M": g.M, "nnz": g.nnz, "in": 128, "hidden": 256, "classes": 47,
+           "spmm_flops_per_step": 2.0 * g.nnz * (256 + 47) * 2}
+    for backend in backends:
+        torch.manual_seed(1)
+        graph = gnn.GraphBackend(op, "cuda", table)
+        model = gnn.GCN(128, 256, 47).cuda()
+        opt = torch.optim.Adam(model.parameters(), lr=1e-2)
+        t0 = time.perf_counter()
+        cold = gnn.train_step(model, graph, backend, X, y, opt)
+        setup = time.perf_counter() - t0
+        for _ in range(warmup):
+            gnn.train_step(model, graph, backend, X, y, opt)
+        ts = [gnn.train_step(model, graph, backend, X, y, opt) for _ in range(steps)]
+        ms = 1e3 * sum(ts) / len(ts)
+        rec = {"step_ms": ms, "cold_first_step_ms": cold * 1e3}
+        if backend == "router":
+            rec["paths"] = {f"{'bwd' if t else 'fwd'}_N{n}": lab
+                            for (b, t, n), (lab, _) in graph.exec_cache.items()}
+        out[backend] = rec
+        log(f"[gcn] {backend:14s} step {ms:8.3f} ms  cold first step {cold * 1e3:9.1f} ms "
+            f"{rec.get('paths', '')}")
+        del graph, model, opt
+        torch.cuda.empty_cache()
+    return out
+
+
 def sweep(configs, Ns, steps, out_path):
     """Every deployed path on each config (calibration of the MI355X table)."""
     import torch
@@ -269,6 +309,7 @@ def main(argv=None):
     ap.add_argument("--details", default=None, help="write the full result dict here")
     ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
     ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
+    ap.add_argument("--gcn", action="store_true", help="config 5 GCN training step (details on stderr)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -280,6 +321,12 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 3
+    if args.gcn:
+        res = bench_gcn(max(5, args.steps // 20), max(2, args.warmup // 10), args.table)
+        if args.details:
+            Path(args.details).parent.mkdir(parents=True, exist_ok=True)
+            Path(args.details).write_text(json.dumps(res, indent=1))
+        return 0
     if args.sweep:
         sweep(args.sweep.split(","), [int(n) for n in args.sweep_N.split(",")], max(10, args.steps // 4),
               args.sweep_out)

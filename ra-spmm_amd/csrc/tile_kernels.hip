@@ -25,6 +25,7 @@
 //            tc/ra_tc_direct.cu:85-104.
 #include <algorithm>
 #include <chrono>
+#include <cstdlib>
 
 #include "ra_internal.hpp"
 #include "tile_format.hpp"
@@ -99,21 +100,40 @@ __device__ __forceinline__ float* item_row(const Items& it, float* C, float* scr
     return C + (int64_t)row * N;
 }
 
+// 1-D grid: block -> (group of 4 items, column slice), slice fastest, so all
+// slices of a window run back to back and share its atox/vals in L2.  With
+// remap on, each XCD (workgroups are dealt round-robin over 8) takes one
+// contiguous range of windows, keeping neighbouring windows in one L2.
+__device__ __forceinline__ void tile_block_coords(int nslices, bool remap, int64_t& item_blk,
+                                                  int& slice) {
+    int64_t bid = blockIdx.x;
+    if (remap) {
+        const int64_t nb = gridDim.x, q = nb / 8, r = nb % 8, x = bid % 8, k = bid / 8;
+        bid = x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+    }
+    item_blk = bid / nslices;
+    slice = static_cast<int>(bid - item_blk * nslices);
+}
+
 // ------------------------------------------------------------ MFMA route
 template <int CPL, bool BF16, int KIND>
 __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ Bh, int ldb, float* __restrict__ C, float* __restrict__ scratch,
-    int M, int N, int num_items) {
+    int M, int N, int num_items, int nslices, int remap) {
     typedef typename HalfRun<CPL>::T Run;
     const int lane = threadIdx.x & (kWave - 1);
-    const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
+    int64_t item_blk;
+    int slice;
+    tile_block_coords(nslices, remap != 0, item_blk, slice);
+    const int item = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
     int w, b0, b1, slot;
     item_range<KIND>(it, item, w, b0, b1, slot);
     const int j = lane & 15;
     const int q = lane >> 4;
-    const int col = blockIdx.y * (16 * CPL) + j * CPL;
+    const int col = slice * (16 * CPL) + j * CPL;
     const bool col_ok = col < ldb;  // ldb % 8 == 0 and CPL | 8: whole run in bounds
     const bool a_half = (j < 8) == (q < 2);
 
@@ -183,13 +203,17 @@ template <int F, bool VEC, int KIND>
 __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
     Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
     const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch, int M, int N,
-    int num_items) {
+    int num_items, int nslices, int remap) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int item = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
+    int64_t item_blk;
+    int slice;
+    tile_block_coords(nslices, remap != 0, item_blk, slice);
+    const int item = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
     int w, b0, b1, slot;
     item_range<KIND>(it, item, w, b0, b1, slot);
-    const int col = blockIdx.y * (64 * F) + lane * F;
+    const int col = slice * (64 * F) + lane * F;
     float acc[8][F];
 #pragma unroll
     for (int r = 0; r < 8; ++r)
@@ -260,8 +284,9 @@ __global__ __launch_bounds__(kBlock) void tile_merge_kernel(
 
 // --------------------------------------------------------------- convert
 // fp32 [rows, cols] -> 16-bit [rows, ldo], RNE, columns cols..ldo-1 zeroed.
-// One thread writes 8 consecutive outputs (one 16-byte store).
-template <bool BF16>
+// One thread writes 8 consecutive outputs (one 16-byte store); VEC reads them
+// as two 16-byte loads (cols % 8 == 0, 16-byte aligned input).
+template <bool BF16, bool VEC>
 __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict__ in,
                                                          uint16_t* __restrict__ out, int64_t rows,
                                                          int cols, int ldo) {
@@ -272,12 +297,24 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
         const int64_t r = g / groups;
         const int c0 = static_cast<int>(g - r * groups) * 8;
         const float* src = in + r * cols;
+        float x[8];
+        if constexpr (VEC) {
+            const f32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + c0));
+            const f32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + c0 + 4));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[i] = lo[i];
+                x[4 + i] = hi[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = (c0 + i < cols) ? src[c0 + i] : 0.f;
+        }
         u16x8 o;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float x = (c0 + i < cols) ? src[c0 + i] : 0.f;
-            if constexpr (BF16) o[i] = __builtin_bit_cast(unsigned short, static_cast<__bf16>(x));
-            else o[i] = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x));
+            if constexpr (BF16) o[i] = __builtin_bit_cast(unsigned short, static_cast<__bf16>(x[i]));
+            else o[i] = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x[i]));
         }
         *reinterpret_cast<u16x8*>(out + r * ldo + c0) = o;
     }
@@ -288,10 +325,12 @@ ra_status launch_convert(const float* in, void* out, int64_t rows, int32_t cols,
     if (rows <= 0 || ldo <= 0) return RA_OK;
     const int64_t total = rows * (ldo / 8);
     const int blocks = static_cast<int>(std::min<int64_t>((total + kBlock - 1) / kBlock, 1 << 16));
-    if (bf16)
-        convert_kernel<true><<<blocks, kBlock, 0, st>>>(in, static_cast<uint16_t*>(out), rows, cols, ldo);
-    else
-        convert_kernel<false><<<blocks, kBlock, 0, st>>>(in, static_cast<uint16_t*>(out), rows, cols, ldo);
+    const bool vec = (cols % 8 == 0) && ldo == cols && ra::aligned16(in);
+    uint16_t* o = static_cast<uint16_t*>(out);
+    if (bf16 && vec) convert_kernel<true, true><<<blocks, kBlock, 0, st>>>(in, o, rows, cols, ldo);
+    else if (bf16) convert_kernel<true, false><<<blocks, kBlock, 0, st>>>(in, o, rows, cols, ldo);
+    else if (vec) convert_kernel<false, true><<<blocks, kBlock, 0, st>>>(in, o, rows, cols, ldo);
+    else convert_kernel<false, false><<<blocks, kBlock, 0, st>>>(in, o, rows, cols, ldo);
     RA_LAUNCH_CHECK("convert_kernel");
     return RA_OK;
 }
@@ -310,6 +349,15 @@ struct ra_tile_plan {
 
 namespace {
 
+// RA_TILE_XCD_REMAP=0 turns the XCD-contiguous window order off.
+int tile_remap() {
+    static const int r = [] {
+        const char* e = std::getenv("RA_TILE_XCD_REMAP");
+        return e ? (std::atoi(e) != 0) : 1;
+    }();
+    return r;
+}
+
 Items plan_items(const ra_tile_plan* p) {
     Items it{};
     it.block_offsets = p->block_offsets.get<int32_t>();
@@ -327,15 +375,17 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
     const int M = p->info.M;
     const Items it = plan_items(p);
     const int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
-    dim3 grid((p->num_items + kWavesPerBlock - 1) / kWavesPerBlock, (N + 16 * cpl - 1) / (16 * cpl));
+    const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
+    const int remap = tile_remap();
+    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
 #define RA_MFMA_CASE(c)                                                                            \
     if (cpl == c) {                                                                                \
         if (bf16)                                                                                  \
             tile_mfma_kernel<c, true, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),    \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items);                 \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap); \
         else                                                                                       \
             tile_mfma_kernel<c, false, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),   \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items);                 \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap); \
     }
     RA_MFMA_CASE(1)
     RA_MFMA_CASE(2)
@@ -353,7 +403,9 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
     const Items it = plan_items(p);
     const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
     const bool vec = (N % F == 0) && ((reinterpret_cast<uintptr_t>(B) % (4 * F)) == 0);
-    dim3 grid((p->num_items + kWavesPerBlock - 1) / kWavesPerBlock, (N + 64 * F - 1) / (64 * F));
+    const int nslices = (N + 64 * F - 1) / (64 * F);
+    const int remap = tile_remap();
+    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int bf = p->info.value_dtype == RA_DTYPE_BF16;
     const int32_t* ax = p->atox.get<int32_t>();
     const uint16_t* vl = p->vals.get<uint16_t>();
@@ -361,10 +413,10 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
     if (F == f) {                                                                                    \
         if (vec)                                                                                     \
             tile_fp32_kernel<f, true, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, B, C, scratch, M, N, \
-                                                                   p->num_items);                   \
+                                                                   p->num_items, nslices, remap);   \
         else                                                                                         \
             tile_fp32_kernel<f, false, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, B, C, scratch, M, N, \
-                                                                    p->num_items);                  \
+                                                                    p->num_items, nslices, remap);  \
     }
     RA_FP32_CASE(1)
     RA_FP32_CASE(2)

@@ -1,0 +1,252 @@
+"""GNN call site of the routed SpMM: graph backend, autograd SpMM and GCN.
+
+Reference: gnn_bench/router_vs_baselines_gcn.py — build_aggregation_operator
+(:89-126), GraphBackend (:162-410), validate_backend (:413-445),
+SparseMMFunction (:451-461), GCNBench (:464-476), measure_step (:482-498);
+cold first-step policy gnn_bench/cold_first_step.py:61-139 (route, then run
+CSR_DIRECT without building any plan).
+
+A GraphBackend owns the CSR of A and of A^T on the device, one router plan
+per (transpose, N) and one executor (path label + plan) per
+(backend, transpose, N).  Backends:
+  "router"        MI355X router (default table), plan built on first use
+  "router_cold"   first call per (transpose, N): feature pass + route, then
+                  CSR_DIRECT with no plan build; later calls as "router"
+  "cusparse"      the guardrail name, served by the baseline CSR kernel
+  "csr_direct", "zero_overhead", "tc_direct", "tc_direct_tf32",
+  "community_tc", "segment_hybrid"   fixed paths
+  "torch"         torch.sparse CSR on the device (external comparison only)
+"""
+from __future__ import annotations
+
+import math
+import time
+from typing import Dict, Tuple
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _C
+from .dispatch import TILE_KERNELS, build_kernel_plan, run_planned_kernel
+from .router import route_label
+
+BASE_ATOL = 1e-3        # ra_real_graph_eval.py:41-51
+TC_EXTRA_FACTOR = 10.0
+
+_FIXED = {"csr_direct": "CSR_DIRECT", "zero_overhead": "ZERO_OVERHEAD_CSR",
+          "tc_direct": "TC_DIRECT", "tc_direct_tf32": "TC_DIRECT_TF32",
+          "community_tc": "COMMUNITY_TC", "segment_hybrid": "SEGMENT_HYBRID"}
+
+
+def build_aggregation_operator(csr, model: str):
+    """Per-model aggregation matrix (scipy CSR, fp32, sorted indices):
+    GCN  D~^-1/2 (A + I) D~^-1/2 (self-loop added only where absent),
+    SAGE D^-1 A (zero-degree rows stay zero), GIN A unchanged."""
+    import scipy.sparse as sp
+    A = csr.tocsr().astype(np.float64)
+    A.sum_duplicates()
+    m = model.lower()
+    if m == "gin":
+        out = A.copy()
+    elif m in ("graphsage", "sage"):
+        deg = np.asarray(A.sum(axis=1)).ravel()
+        dinv = np.divide(1.0, deg, out=np.zeros_like(deg), where=deg > 0)
+        out = sp.diags(dinv) @ A
+    elif m == "gcn":
+        eye = sp.eye(A.shape[0], format="csr", dtype=np.float64)
+        eye.data[A.diagonal() != 0] = 0.0
+        Ahat = (A + eye).tocsr()
+        Ahat.eliminate_zeros()
+        d = np.asarray(Ahat.sum(axis=1)).ravel()
+        dis = np.divide(1.0, np.sqrt(d), out=np.zeros_like(d), where=d > 0)
+        D = sp.diags(dis)
+        out = D @ Ahat @ D
+    else:
+        raise ValueError(f"unknown model for aggregation operator: {model}")
+    out = out.tocsr().astype(np.float32)
+    out.sort_indices()
+    return out
+
+
+def operator_descriptors(csr) -> Dict[str, float]:
+    """M, nnz, d_bar, population CV of row lengths."""
+    deg = np.diff(csr.indptr).astype(np.float64)
+    M = int(csr.shape[0])
+    mean = deg.mean() if M else 0.0
+    return {"M": M, "nnz": int(csr.indptr[-1]), "d_bar": float(mean),
+            "cv_d": float(deg.std() / mean) if mean > 0 else 0.0}
+
+
+def _tensors(csr, device):
+    return {
+        "rowptr_cpu": torch.from_numpy(csr.indptr.astype(np.int32)),
+        "colind_cpu": torch.from_numpy(csr.indices.astype(np.int32)),
+        "vals_cpu": torch.from_numpy(csr.data.astype(np.float32)),
+        "rowptr": torch.from_numpy(csr.indptr.astype(np.int32)).to(device),
+        "colind": torch.from_numpy(csr.indices.astype(np.int32)).to(device),
+        "vals": torch.from_numpy(csr.data.astype(np.float32)).to(device),
+    }
+
+
+class GraphBackend:
+    def __init__(self, csr, device, table: str = "mi355x"):
+        self.device = torch.device(device)
+        self.table = table
+        self.csr = csr.tocsr()
+        self.csr_t = self.csr.transpose().tocsr()
+        self.forward = _tensors(self.csr, self.device)
+        self.backward = _tensors(self.csr_t, self.device)
+        self.plan_cache: Dict[Tuple[bool, int], dict] = {}
+        self.exec_cache: Dict[Tuple[str, bool, int], tuple] = {}
+        self._torch_sparse: Dict[bool, torch.Tensor] = {}
+        self._cold_seen: set = set()
+
+    def _tensors(self, transpose: bool):
+        return self.backward if transpose else self.forward
+
+    def get_router_plan(self, transpose: bool, ncols: int) -> dict:
+        key = (transpose, int(ncols))
+        if key not in self.plan_cache:
+            t = self._tensors(transpose)
+            M = int(t["rowptr"].numel()) - 1
+            # Device rowptr: the feature pass runs on the GPU.
+            self.plan_cache[key] = _C.make_router_plan(t["rowptr"], t["colind"], t["vals"], M, M,
+                                                       int(ncols), "MAIN", self.table)
+        return self.plan_cache[key]
+
+    def routed_label(self, transpose: bool, ncols: int) -> str:
+        return route_label(self.get_router_plan(transpose, ncols))
+
+    def _get_executor(self, backend: str, transpose: bool, ncols: int):
+        key = (backend, transpose, int(ncols))
+        if key in self.exec_cache:
+            return self.exec_cache[key]
+        t = self._tensors(transpose)
+        M = int(t["rowptr"].numel()) - 1
+        if backend == "cusparse":
+            tmpl = torch.empty((M, int(ncols)), device=self.device, dtype=torch.float32)
+            ex = ("CUSPARSE", _C.make_cusparse_plan(t["rowptr"], t["colind"], t["vals"], tmpl))
+        elif backend == "torch":
+            ex = ("torch", None)
+        else:
+            if backend in ("router", "router_cold"):
+                label = self.routed_label(transpose, ncols)
+            elif backend in _FIXED:
+                label = _FIXED[backend]
+            else:
+                raise ValueError(f"Unknown backend {backend}")
+            if label in TILE_KERNELS and int(ncols) < 16:
+                label = "CSR_DIRECT"
+            if label == "CUSPARSE":
+                tmpl = torch.empty((M, int(ncols)), device=self.device, dtype=torch.float32)
+                ex = (label, _C.make_cusparse_plan(t["rowptr"], t["colind"], t["vals"], tmpl))
+            else:
+                # Tile plans are N-independent (N only gates N >= 16): share one
+                # plan per (family, transpose) across widths and precisions.
+                plan = None
+                if label in TILE_KERNELS:
+                    fam = label.replace("_TF32", "")
+                    for (b, tr, n), (lab, p) in self.exec_cache.items():
+                        if tr == transpose and lab.replace("_TF32", "") == fam and p is not None:
+                            plan = p
+                            break
+                if plan is None:
+                    plan = build_kernel_plan(label, t["rowptr_cpu"], t["colind_cpu"],
+                                             t["vals_cpu"], M, M, max(int(ncols), 16))
+                ex = (label, plan)
+        self.exec_cache[key] = ex
+        return ex
+
+    def run(self, B: torch.Tensor, backend: str, transpose: bool = False) -> torch.Tensor:
+        t = self._tensors(transpose)
+        ncols = int(B.shape[1])
+        if backend == "router_cold" and (transpose, ncols) not in self._cold_seen:
+            # Cold first call: feature pass + route, then CSR_DIRECT, no plan build.
+            self._cold_seen.add((transpose, ncols))
+            self.get_router_plan(transpose, ncols)
+            return _C.spmm_csr_direct(t["rowptr"], t["colind"], t["vals"], B)
+        label, plan = self._get_executor(backend, transpose, ncols)
+        if label == "CUSPARSE":
+            return _C.run_cusparse_plan(plan, B).clone()
+        if label == "torch":
+            if transpose not in self._torch_sparse:
+                M = int(t["rowptr"].numel()) - 1
+                self._torch_sparse[transpose] = torch.sparse_csr_tensor(
+                    t["rowptr"].long(), t["colind"].long(), t["vals"], size=(M, M))
+            return torch.sparse.mm(self._torch_sparse[transpose], B)
+        return run_planned_kernel(label, plan, t["rowptr"], t["colind"], t["vals"], B)
+
+
+def validate_backend(csr, device, backend: str, ncols_values, seed: int, table="mi355x"):
+    """Every (transpose, N) SpMM of a fresh backend against the baseline kernel
+    with the reference's gate (ra_real_graph_eval.py:41-51)."""
+    graph = GraphBackend(csr, device, table)
+    max_err = max_tol = 0.0
+    for transpose in (False, True):
+        t = graph._tensors(transpose)
+        deg = t["rowptr_cpu"][1:] - t["rowptr_cpu"][:-1]
+        max_row = max(1, int(deg.max().item())) if deg.numel() else 1
+        for ncols in sorted(set(int(v) for v in ncols_values)):
+            torch.manual_seed(seed + ncols + int(transpose))
+            B = torch.randn((csr.shape[0], ncols), device=device)
+            out = graph.run(B, backend, transpose)
+            ref = _C.spmm_cusparse(t["rowptr"], t["colind"], t["vals"], B)
+            err = float((out.float() - ref).abs().max().item())
+            path = graph._get_executor(backend, transpose, ncols)[0]
+            tol = BASE_ATOL * max(1.0, math.sqrt(max_row))
+            if path in TILE_KERNELS:
+                tol *= TC_EXTRA_FACTOR
+            max_err, max_tol = max(max_err, err), max(max_tol, tol)
+            if err > tol or err >= 1.0:
+                return {"correct": False, "soft_fail": tol < err < 1.0, "hard_fail": err >= 1.0,
+                        "max_error": err, "tolerance": tol, "path": path}
+    return {"correct": True, "soft_fail": False, "hard_fail": False, "max_error": max_err,
+            "tolerance": max_tol}
+
+
+class SparseMMFunction(torch.autograd.Function):
+    """Y = A @ B; dL/dB = A^T @ dL/dY (gnn_bench/router_vs_baselines_gcn.py:451-461)."""
+
+    @staticmethod
+    def forward(ctx, B, graph: GraphBackend, backend: str):
+        ctx.graph = graph
+        ctx.backend = backend
+        return graph.run(B.contiguous(), backend, transpose=False)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return ctx.graph.run(grad_output.contiguous(), ctx.backend, transpose=True), None, None
+
+
+class GCN(nn.Module):
+    """2-layer GCN: A relu(A X W1) W2 (gnn_bench/router_vs_baselines_gcn.py:464-476)."""
+
+    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int):
+        super().__init__()
+        self.lin1 = nn.Linear(in_dim, hidden_dim, bias=False)
+        self.lin2 = nn.Linear(hidden_dim, out_dim, bias=False)
+
+    def forward(self, X, graph: GraphBackend, backend: str):
+        h = SparseMMFunction.apply(self.lin1(X), graph, backend)
+        h = F.relu(h)
+        return SparseMMFunction.apply(self.lin2(h), graph, backend)
+
+
+GCNBench = GCN
+
+
+def train_step(model, graph, backend, X, y, optimizer) -> float:
+    """One forward + backward + optimizer step; seconds (synchronised)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    optimizer.zero_grad(set_to_none=True)
+    loss = F.cross_entropy(model(X, graph, backend), y)
+    loss.backward()
+    optimizer.step()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+measure_step = train_step

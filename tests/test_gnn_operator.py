@@ -1,0 +1,36 @@
+"""The GCN aggregation operator (CPU): build_aggregation_operator (scipy,
+gnn_bench/router_vs_baselines_gcn.py:89-126) and the synthetic generator's
+gcn_operator agree, and both satisfy the closed form D^-1/2 (A+I) D^-1/2."""
+import numpy as np
+import scipy.sparse as sp
+
+from ra_spmm import synthetic as S
+from ra_spmm.gnn import build_aggregation_operator, operator_descriptors
+
+
+def test_gcn_operator_closed_form_and_agreement():
+    g = S.chung_lu(3000, 6.0, 2.3, 300, seed=9)
+    A = sp.csr_matrix((np.ones(g.nnz, np.float32), g.colind, g.rowptr), shape=(g.M, g.M))
+    op = build_aggregation_operator(A, "gcn")
+    h = S.gcn_operator(g)
+    np.testing.assert_array_equal(op.indptr, h.rowptr)
+    np.testing.assert_array_equal(op.indices, h.colind)
+    np.testing.assert_allclose(op.data, h.vals, rtol=1e-6)
+    dense = A.toarray().astype(np.float64) + np.eye(g.M)
+    d = dense.sum(1)
+    ref = dense / np.sqrt(d)[:, None] / np.sqrt(d)[None, :]
+    np.testing.assert_allclose(op.toarray(), ref, rtol=1e-6, atol=1e-9)
+    desc = operator_descriptors(op)
+    assert desc["M"] == g.M and desc["nnz"] == g.nnz + g.M
+
+
+def test_sage_and_gin_operators():
+    g = S.random_csr(50, 50, 4.0, seed=2, empty_frac=0.1)
+    A = sp.csr_matrix((np.abs(g.vals), g.colind, g.rowptr), shape=(50, 50))
+    gin = build_aggregation_operator(A, "gin")
+    np.testing.assert_allclose(gin.toarray(), A.toarray(), rtol=1e-7)
+    sage = build_aggregation_operator(A, "sage").toarray()
+    rs = A.toarray().sum(1)
+    nz = rs > 0
+    np.testing.assert_allclose(sage[nz].sum(1), 1.0, rtol=1e-6)
+    assert np.all(sage[~nz] == 0)

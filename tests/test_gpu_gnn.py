@@ -1,0 +1,79 @@
+"""GNN call site on the GPU: GraphBackend per (transpose, N) routing, the
+autograd SpMM (backward through A^T) and a 2-layer GCN step, against the
+baseline kernel and a dense fp32 torch reference."""
+import numpy as np
+import pytest
+import scipy.sparse as sp
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+from ra_spmm import synthetic as S  # noqa: E402
+from ra_spmm import gnn  # noqa: E402
+
+
+def _operator(M=4000, seed=3):
+    g = S.chung_lu(M, 12.0, 2.3, 600, seed=seed)
+    A = sp.csr_matrix((np.ones(g.nnz, np.float32), g.colind, g.rowptr), shape=(M, M))
+    return gnn.build_aggregation_operator(A, "gcn")
+
+
+@pytest.mark.parametrize("backend", ["router", "router_cold", "cusparse", "csr_direct",
+                                     "zero_overhead", "tc_direct", "tc_direct_tf32",
+                                     "segment_hybrid"])
+def test_validate_backend(backend):
+    op = _operator()
+    res = gnn.validate_backend(op, "cuda", backend, (16, 47, 64, 256), seed=1)
+    assert res["correct"], res
+
+
+def test_gcn_step_matches_dense_reference():
+    op = _operator(3000, seed=5)
+    M = op.shape[0]
+    torch.manual_seed(0)
+    X = torch.randn(M, 32, device="cuda")
+    y = torch.randint(0, 7, (M,), device="cuda")
+    dense = torch.from_numpy(op.toarray()).cuda()
+    results = {}
+    for backend in ("cusparse", "router", "zero_overhead", "csr_direct", "segment_hybrid"):
+        torch.manual_seed(1)
+        model = gnn.GCN(32, 64, 7).cuda()
+        graph = gnn.GraphBackend(op, "cuda")
+        out = model(X, graph, backend)
+        loss = F.cross_entropy(out, y)
+        loss.backward()
+        fp16 = any(lab in gnn.TILE_KERNELS and not lab.endswith("_TF32")
+                   for lab, _ in graph.exec_cache.values())
+        results[backend] = (out.detach(), [p.grad.detach().clone() for p in model.parameters()], fp16)
+    torch.manual_seed(1)
+    ref_model = gnn.GCN(32, 64, 7).cuda()
+    h = F.relu(dense @ ref_model.lin1(X))
+    ref_out = dense @ ref_model.lin2(h)
+    F.cross_entropy(ref_out, y).backward()
+    ref_grads = [p.grad for p in ref_model.parameters()]
+    for backend, (out, grads, fp16) in results.items():
+        # fp32 paths: accumulation-order differences only; fp16 tile paths round
+        # A and the dense operand to fp16 (2^-11 relative each).
+        rtol, atol = (2e-2, 2e-3) if fp16 else (2e-4, 2e-5)
+        torch.testing.assert_close(out, ref_out, rtol=rtol, atol=atol, msg=backend)
+        for g_, r_ in zip(grads, ref_grads):
+            torch.testing.assert_close(g_, r_, rtol=10 * rtol, atol=atol, msg=backend)
+
+
+def test_router_plans_per_transpose_and_width():
+    op = _operator(5000, seed=7)
+    graph = gnn.GraphBackend(op, "cuda")
+    labels = {(t, n): graph.routed_label(t, n) for t in (False, True) for n in (47, 256)}
+    assert len(graph.plan_cache) == 4
+    for (t, n), lab in labels.items():
+        assert lab in ("CSR_DIRECT", "ZERO_OVERHEAD_CSR", "CUSPARSE", "TC_DIRECT", "COMMUNITY_TC",
+                       "SEGMENT_HYBRID", "TC_DIRECT_TF32", "COMMUNITY_TC_TF32",
+                       "SEGMENT_HYBRID_TF32")
+    model = gnn.GCN(16, 256, 47).cuda()
+    opt = torch.optim.Adam(model.parameters(), lr=1e-2)
+    X = torch.randn(op.shape[0], 16, device="cuda")
+    y = torch.randint(0, 47, (op.shape[0],), device="cuda")
+    for _ in range(3):
+        dt = gnn.train_step(model, graph, "router", X, y, opt)
+        assert dt > 0
