@@ -213,6 +213,19 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
     return res
 
 
+def profile_traffic(kernel: str, cfg: str, N: int):
+    """HBM bytes per launch of `kernel` on (cfg, N) from the committed rocprofv3
+    summary profiles/<kernel>_<cfg>_N<N>.md (FETCH_SIZE + WRITE_SIZE, each
+    scaled by a 1 GiB copy probe), or None when no summary exists."""
+    path = ROOT / "profiles" / f"{kernel}_{cfg}_N{N}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def bench_gcn(steps, warmup, table, backends=("router", "cusparse", "zero_overhead", "csr_direct")):
     """2-layer GCN training step (128 -> 256 -> 47) on the
     synthetic power-law operator, forward A X and backward A^T G routed per
@@ -347,7 +360,8 @@ def main(argv=None):
                    "N": res["N"], "router_table": args.table},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": args.traffic, "kernel": res["kernel"],
+                     "traffic": args.traffic if args.traffic is not None else
+                     profile_traffic(res["kernel"], args.config, res["N"]), "kernel": res["kernel"],
                      "kernel_ms": round(res["kernel_ms"], 5), "bytes_alg": res["bytes_alg"]},
         "cpu_baseline": res.get("cpu_port"),
         "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),

@@ -141,21 +141,30 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
 #pragma unroll
     for (int cc = 0; cc < CPL; ++cc) acc[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int b = b0; b < b1; b += 4) {
+    // Indices and A fragment of step b (block b+q of this lane group).
+    auto load_step = [&](int b, int (&cols)[8], u16x8& a) {
         const int bq = b + q;
-        const bool bok = bq < b1;
-        int cols[8];
-        if (bok) {
+        if (bq < b1) {
             const int4 c0 = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8);
             const int4 c1 = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8 + 4);
             cols[0] = c0.x; cols[1] = c0.y; cols[2] = c0.z; cols[3] = c0.w;
             cols[4] = c1.x; cols[5] = c1.y; cols[6] = c1.z; cols[7] = c1.w;
+            a = a_half ? *reinterpret_cast<const u16x8*>(vals + (int64_t)bq * 64 + (j & 7) * 8)
+                       : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         } else {
 #pragma unroll
             for (int v = 0; v < 8; ++v) cols[v] = -1;
+            a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         }
-        u16x8 a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (bok && a_half) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)bq * 64 + (j & 7) * 8);
+    };
+    int cols_next[8];
+    u16x8 a_next;
+    if (b0 < b1) load_step(b0, cols_next, a_next);
+    for (int b = b0; b < b1; b += 4) {
+        int cols[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) cols[v] = cols_next[v];
+        const u16x8 a = a_next;
         Run raw[8];
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
@@ -164,6 +173,9 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
             else
                 raw[v] = Run{};
         }
+        // Prefetch the next step's indices while this step's gathers are in
+        // flight: the atox -> B dependency leaves the critical path.
+        if (b + 4 < b1) load_step(b + 4, cols_next, a_next);
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc) {
             u16x8 bop;
@@ -221,35 +233,40 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
         for (int f = 0; f < F; ++f) acc[r][f] = 0.f;
     const bool bf = bf16vals != 0;
     for (int b = b0; b < b1; ++b) {
+        // All 8 indices of the block first (wave-uniform), then all 8 gathers,
+        // then the FMAs in vector (= ascending column) order.
+        int c[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) c[v] = atox[(int64_t)b * 8 + v];
+        float bv[8][F];
+#pragma unroll
         for (int v = 0; v < 8; ++v) {
-            const int c = atox[(int64_t)b * 8 + v];
-            if (c < 0) break;  // padding sits at the end of the last block
-            float bv[F];
-            if constexpr (VEC) {
-                if (col < N) {
-                    if constexpr (F == 4) {
-                        const float4 t = *reinterpret_cast<const float4*>(B + (int64_t)c * N + col);
-                        bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
-                    } else if constexpr (F == 2) {
-                        const float2 t = *reinterpret_cast<const float2*>(B + (int64_t)c * N + col);
-                        bv[0] = t.x; bv[1] = t.y;
-                    } else {
-                        bv[0] = B[(int64_t)c * N + col];
-                    }
+            if (c[v] >= 0 && col < N) {
+                const float* src = B + (int64_t)c[v] * N + col;
+                if constexpr (VEC && F == 4) {
+                    const float4 t = *reinterpret_cast<const float4*>(src);
+                    bv[v][0] = t.x; bv[v][1] = t.y; bv[v][2] = t.z; bv[v][3] = t.w;
+                } else if constexpr (VEC && F == 2) {
+                    const float2 t = *reinterpret_cast<const float2*>(src);
+                    bv[v][0] = t.x; bv[v][1] = t.y;
                 } else {
 #pragma unroll
-                    for (int f = 0; f < F; ++f) bv[f] = 0.f;
+                    for (int f = 0; f < F; ++f) bv[v][f] = (col + f < N) ? src[f] : 0.f;
                 }
             } else {
 #pragma unroll
-                for (int f = 0; f < F; ++f) bv[f] = (col + f < N) ? B[(int64_t)c * N + col + f] : 0.f;
+                for (int f = 0; f < F; ++f) bv[v][f] = 0.f;
             }
-            const uint16_t* vb = vals + (int64_t)b * 64 + v;
+        }
+        const uint16_t* vb = vals + (int64_t)b * 64;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            if (c[v] < 0) break;  // padding sits at the end of the last block
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                const float a = stored_to_f32(vb[r * 8], bf);
+                const float a = stored_to_f32(vb[r * 8 + v], bf);
 #pragma unroll
-                for (int f = 0; f < F; ++f) acc[r][f] = __builtin_fmaf(a, bv[f], acc[r][f]);
+                for (int f = 0; f < F; ++f) acc[r][f] = __builtin_fmaf(a, bv[v][f], acc[r][f]);
             }
         }
     }
@@ -358,6 +375,17 @@ int tile_remap() {
     return r;
 }
 
+// RA_TILE_CPL caps the columns per lane of the MFMA kernel (1, 2, 4 or 8):
+// fewer columns per lane = fewer registers = more resident waves.
+int tile_max_cpl() {
+    static const int c = [] {
+        const char* e = std::getenv("RA_TILE_CPL");
+        const int v = e ? std::atoi(e) : 8;
+        return v >= 8 ? 8 : v >= 4 ? 4 : v >= 2 ? 2 : 1;
+    }();
+    return c;
+}
+
 Items plan_items(const ra_tile_plan* p) {
     Items it{};
     it.block_offsets = p->block_offsets.get<int32_t>();
@@ -374,7 +402,8 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
                            float* scratch, int N, hipStream_t st) {
     const int M = p->info.M;
     const Items it = plan_items(p);
-    const int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
+    int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
+    cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
     const int remap = tile_remap();
     dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
