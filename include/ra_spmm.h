@@ -245,6 +245,8 @@ typedef struct ra_tile_info {
     float avg_tile_density;    /* nnz / (8 * 8 * num_blocks)               */
     int32_t value_dtype;       /* RA_DTYPE_F16 or RA_DTYPE_BF16            */
     double build_ms;           /* host build + upload                      */
+    int32_t value_scale_log2;  /* fp16 plans store v * 2^s (s chosen from   */
+    int32_t pad2_;             /* max|v|), outputs are scaled back by 2^-s */
 } ra_tile_info;
 
 /* Host-only build of the tile format (testable without a GPU).

@@ -130,6 +130,27 @@ def quantize_f16(x) -> np.ndarray:
     return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
+def tile_value_scale_log2(vals) -> int:
+    """Power-of-two exponent s the fp16 tile plans store values with (v * 2^s):
+    max|v| lands in [2^13, 2^14), clamped to [-24, 24]; 0 for an all-zero
+    matrix.  Pinned by tests/test_oracle_structures.py against the builder and
+    by the closed form on powers of two."""
+    a = np.abs(np.asarray(vals, dtype=np.float32))
+    if a.size == 0 or not np.isfinite(a).all() or a.max() == 0:
+        return 0
+    e = int(np.floor(np.log2(np.float64(a.max()))))
+    return int(min(24, max(-24, 13 - e)))
+
+
+def quantize_f16_scaled(x, s: int) -> np.ndarray:
+    """fp16 RNE of x * 2^s, returned as fp32 times 2^-s (exact power-of-two
+    scaling: identical to quantize_f16 for normal-range values, more precise
+    for values that would be fp16 subnormals)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (np.ldexp(x, s).astype(np.float16).astype(np.float32) * np.float32(2.0 ** -s)).astype(np.float32)
+
+
 def quantize_bf16(x) -> np.ndarray:
     """bf16 round-to-nearest-even (NaN kept quiet), returned as fp32."""
     u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
@@ -475,16 +496,18 @@ def tile_decode(fmt, M, K):
 
 def spmm_tile_f64(rowptr, colind, vals, B, route: str):
     """Exact value of a tile path's output: vals quantised like the plan
-    (fp16 for F16 and FP32 routes, bf16 for BF16), B quantised like the route
+    (fp16 with the plan's power-of-two scale for F16 and FP32 routes, bf16 for
+    BF16), B quantised like the route
     (fp16 / bf16 / unchanged), fp64 accumulation.  The reference FP16 path
     computes the same products exactly (fp16 x fp16 is exact in fp32) and
     differs only in fp32 summation order (tc/ra_tc_direct.cu:109-179)."""
+    sc = tile_value_scale_log2(vals)
     if route == "f16":
-        qv, qb = quantize_f16(vals), quantize_f16(B)
+        qv, qb = quantize_f16_scaled(vals, sc), quantize_f16(B)
     elif route == "bf16":
         qv, qb = quantize_bf16(vals), quantize_bf16(B)
     elif route == "fp32":
-        qv, qb = quantize_f16(vals), np.asarray(B, dtype=np.float32)
+        qv, qb = quantize_f16_scaled(vals, sc), np.asarray(B, dtype=np.float32)
     elif route == "tf32_reference":
         qv, qb = quantize_f16(vals), quantize_tf32_rna(B)
     else:

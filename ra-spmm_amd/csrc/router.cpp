@@ -55,17 +55,23 @@ constexpr RouterTable kReference = {
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 2e-8, 20.0, 5.0f, 25000, 9.0f,
     0, 0, 1e30f};
 
-// MI355X calibration.  Structure of the tree is unchanged; the knobs below are
-// set from the gfx950 sweep (bench.py --calibrate):
-//  - tile gate: host ME-BCRS build plus upload cost per nnz on the MI355X host;
-//  - skewed graphs (cv >= 3) -> hub-chunked ZERO_OVERHEAD_CSR;
-//  - FP32-route tile picks -> the CSR family (the FP32 route reads B in fp32
-//    and pays block padding on wave64);
-//  - CSR_DIRECT picks on skewed rows (cv >= 1.5) -> ZERO_OVERHEAD_CSR.
+// MI355X calibration (structure of the tree unchanged; measured on gfx950 with
+// bench.py --sweep over the five BASELINE configs):
+//  - tile gate: host build + upload of the tile plans runs at 0.75-1.5e-8 s
+//    per nnz on the MI355X host (C2 16e6 nnz: 0.12-0.23 s; C4 1.24e8 nnz:
+//    0.93-1.2 s), so the estimate is 1e-8 s per nnz with the same 20 s budget;
+//  - FP32-route tile picks go to the CSR family: on the ER graph of config 1
+//    CSR_DIRECT takes 9-14 us against 25-42 us for the FP32 tile route;
+//  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR:
+//    one lane group per hub row is 6.6x slower on config 2.
+//  Rules 1-7 otherwise keep the published thresholds: COMMUNITY_TC for
+//  dense/heavy rows (config 4: 16.5 ms, the fastest path), TC_DIRECT for the
+//  uniform family (config 3), ZERO_OVERHEAD_CSR for extreme skew (the fp32
+//  path on configs 2 and 5).
 constexpr RouterTable kMI355X = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-8, 20.0, 5.0f, 25000, 9.0f,
-    1, 1, 1.5f};
+    1, 0, 1.5f};
 
 bool tile_family(int p) {
     return p == RA_PATH_TC_DIRECT || p == RA_PATH_COMMUNITY_TC || p == RA_PATH_SEGMENT_HYBRID;

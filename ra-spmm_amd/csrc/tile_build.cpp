@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <chrono>
 #include <climits>
+#include <cmath>
 #include <cstring>
 #include <numeric>
 
@@ -53,6 +54,15 @@ uint16_t f32_to_bf16_rne(float f) {
     std::memcpy(&x, &f, 4);
     if ((x & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
     return static_cast<uint16_t>((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+int32_t f16_value_scale_log2(float max_abs) {
+    if (!(max_abs > 0.f) || !std::isfinite(max_abs)) return 0;
+    const int e = std::ilogb(max_abs);           // max_abs in [2^e, 2^(e+1))
+    int s = 13 - e;                               // -> [2^13, 2^14)
+    if (s > 24) s = 24;
+    if (s < -24) s = -24;
+    return s;
 }
 
 namespace {
@@ -117,6 +127,12 @@ ra_status tile_host_build(int32_t kind, const int32_t* rowptr, const int32_t* co
     }
 
     const bool bf16 = value_dtype == RA_DTYPE_BF16;
+    if (!bf16) {
+        float mx = 0.f;
+        for (int64_t p = rowptr[0]; p < rowptr[M]; ++p) mx = std::max(mx, std::fabs(vals[p]));
+        out.value_scale_log2 = f16_value_scale_log2(mx);
+    }
+    const float vscale = std::ldexp(1.0f, out.value_scale_log2);
     constexpr int64_t kWinPerTask = 256;
     const int64_t ntasks = (W + kWinPerTask - 1) / kWinPerTask;
     std::vector<WindowRange> parts(ntasks);
@@ -170,7 +186,7 @@ ra_status tile_host_build(int32_t kind, const int32_t* rowptr, const int32_t* co
                     prev_key = e.key;
                 }
                 for (size_t i = 0; i < acc.size(); ++i)
-                    part.vals[vbase + i] = bf16 ? f32_to_bf16_rne(acc[i]) : f32_to_f16_rne(acc[i]);
+                    part.vals[vbase + i] = bf16 ? f32_to_bf16_rne(acc[i]) : f32_to_f16_rne(acc[i] * vscale);
             }
         }
     });
@@ -203,24 +219,26 @@ ra_status tile_host_build(int32_t kind, const int32_t* rowptr, const int32_t* co
         }
     });
 
-    if (kind == RA_TILE_SEGMENT_HYBRID) {
-        // tc/ra_segment_hybrid.cu:470-498: windows of more than 64 blocks are
-        // split into consecutive <= 64-block segments with private partial slots.
+    {
+        // tc/ra_segment_hybrid.cu:470-498: windows of more than `limit` blocks
+        // are split into consecutive <= limit-block segments with private
+        // partial slots, merged in ascending slot order.
+        const int32_t limit = kind == RA_TILE_SEGMENT_HYBRID ? kTileSegBlocks : kTileDirectSplitBlocks;
         out.split_offsets.push_back(0);
         int32_t slots = 0;
         for (int32_t w = 0; w < W; ++w) {
             const int32_t b0 = out.block_offsets[w], b1 = out.block_offsets[w + 1];
-            if (b1 - b0 <= kTileSegBlocks) {
+            if (b1 - b0 <= limit) {
                 out.seg_window.push_back(static_cast<int32_t>(static_cast<uint32_t>(w) | kTileSoleFlag));
                 out.seg_bbegin.push_back(b0);
                 out.seg_bend.push_back(b1);
                 out.seg_slot.push_back(-1);
             } else {
                 out.split_windows.push_back(w);
-                for (int32_t b = b0; b < b1; b += kTileSegBlocks) {
+                for (int32_t b = b0; b < b1; b += limit) {
                     out.seg_window.push_back(w);
                     out.seg_bbegin.push_back(b);
-                    out.seg_bend.push_back(std::min(b + kTileSegBlocks, b1));
+                    out.seg_bend.push_back(std::min(b + limit, b1));
                     out.seg_slot.push_back(slots++);
                 }
                 out.split_offsets.push_back(slots);
@@ -280,6 +298,7 @@ ra_status ra_tile_host_get_info(const ra_tile_host* h, ra_tile_info* info) {
     info->avg_tile_density =
         info->num_blocks > 0 ? static_cast<float>(static_cast<double>(h->nnz) / (64.0 * info->num_blocks)) : 0.f;
     info->value_dtype = h->value_dtype;
+    info->value_scale_log2 = h->value_scale_log2;
     info->build_ms = h->build_ms;
     return RA_OK;
 }

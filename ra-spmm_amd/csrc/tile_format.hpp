@@ -8,9 +8,11 @@
 //   vals[blocks*64]      block values, [block][window slot r][vector k], fp16 or
 //                        bf16 bits.  One 16-byte row per slot is exactly the
 //                        8-element K-run an MFMA 16x16x32 lane consumes.
-//   SEGMENT_HYBRID only: seg_window/seg_bbegin/seg_bend/seg_slot per segment
-//   (bit 31 of seg_window marks a sole segment, seg_slot = -1), and
-//   split_windows/split_offsets for the deterministic merge.
+//   seg_window/seg_bbegin/seg_bend/seg_slot per segment (bit 31 of seg_window
+//   marks a sole segment, seg_slot = -1) and split_windows/split_offsets for
+//   the deterministic merge.  SEGMENT_HYBRID splits windows of more than 64
+//   blocks (the reference rule); the other two kinds only windows of more
+//   than kTileDirectSplitBlocks.
 #pragma once
 
 #include <cstdint>
@@ -24,6 +26,7 @@ struct ra_tile_host {
     int64_t nnz = 0;          // stored entries after duplicate merge
     int64_t num_vectors = 0;  // distinct (window, column) pairs
     int32_t max_window_blocks = 0;
+    int32_t value_scale_log2 = 0;  // fp16 values are stored as v * 2^s
     std::vector<int32_t> win_rows, block_offsets, atox;
     std::vector<uint16_t> vals;
     std::vector<int32_t> seg_window, seg_bbegin, seg_bend, seg_slot, split_windows, split_offsets;
@@ -35,9 +38,17 @@ namespace ra {
 constexpr int kTileWindow = 8;        // rows per window
 constexpr int kTileVec = 8;           // vectors per block
 constexpr int kTileSegBlocks = 64;    // SEGMENT_HYBRID: max blocks per segment
+// TC_DIRECT / COMMUNITY_TC are scheduled the same way with a much larger
+// limit: only extreme (hub) windows are split, so one wave never serialises
+// thousands of blocks while the rest of the GPU idles.
+constexpr int kTileDirectSplitBlocks = 512;
 constexpr uint32_t kTileSoleFlag = 0x80000000u;
 
 uint16_t f32_to_f16_rne(float f);
+// Power-of-two scale 2^s for fp16 storage: maps max|v| near 2^14 so small
+// values (e.g. 1/sqrt(d_i d_j) of hub pairs) stay out of the fp16 subnormal
+// range while leaving 4x headroom below the fp16 maximum.
+int32_t f16_value_scale_log2(float max_abs);
 uint16_t f32_to_bf16_rne(float f);
 
 ra_status tile_host_build(int32_t kind, const int32_t* rowptr, const int32_t* colind,

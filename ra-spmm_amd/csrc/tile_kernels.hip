@@ -25,6 +25,7 @@
 //            tc/ra_tc_direct.cu:85-104.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstdlib>
 
 #include "ra_internal.hpp"
@@ -64,28 +65,21 @@ __device__ __forceinline__ f32x4 mfma32(u16x8 a, u16x8 b, f32x4 c) {
 }
 
 struct Items {
-    const int32_t* block_offsets;  // TC_DIRECT / COMMUNITY_TC
-    const int32_t* seg_window;     // SEGMENT_HYBRID
+    const int32_t* block_offsets;
+    const int32_t* seg_window;
     const int32_t* seg_bbegin;
     const int32_t* seg_bend;
     const int32_t* seg_slot;
     const int32_t* win_rows;       // COMMUNITY_TC
 };
 
-template <int KIND>
+// Work item i = segment i (a whole window unless the window was split).
 __device__ __forceinline__ void item_range(const Items& it, int i, int& w, int& b0, int& b1,
                                            int& slot) {
-    if constexpr (KIND == RA_TILE_SEGMENT_HYBRID) {
-        w = static_cast<int>(static_cast<uint32_t>(it.seg_window[i]) & 0x7FFFFFFFu);
-        b0 = it.seg_bbegin[i];
-        b1 = it.seg_bend[i];
-        slot = it.seg_slot[i];
-    } else {
-        w = i;
-        b0 = it.block_offsets[i];
-        b1 = it.block_offsets[i + 1];
-        slot = -1;
-    }
+    w = static_cast<int>(static_cast<uint32_t>(it.seg_window[i]) & 0x7FFFFFFFu);
+    b0 = it.seg_bbegin[i];
+    b1 = it.seg_bend[i];
+    slot = it.seg_slot[i];
 }
 
 // Destination of window slot m (0..7): a C row, or a partial-slot row.
@@ -120,7 +114,7 @@ template <int CPL, bool BF16, int KIND>
 __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ Bh, int ldb, float* __restrict__ C, float* __restrict__ scratch,
-    int M, int N, int num_items, int nslices, int remap) {
+    int M, int N, int num_items, int nslices, int remap, float unscale) {
     typedef typename HalfRun<CPL>::T Run;
     const int lane = threadIdx.x & (kWave - 1);
     int64_t item_blk;
@@ -130,7 +124,7 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
         static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
     int w, b0, b1, slot;
-    item_range<KIND>(it, item, w, b0, b1, slot);
+    item_range(it, item, w, b0, b1, slot);
     const int j = lane & 15;
     const int q = lane >> 4;
     const int col = slice * (16 * CPL) + j * CPL;
@@ -199,7 +193,7 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
         if (!dst) continue;
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc)
-            if (col + cc < N) dst[col + cc] = acc[cc][r];
+            if (col + cc < N) dst[col + cc] = acc[cc][r] * unscale;  // exact: power of two
     }
 }
 
@@ -214,8 +208,8 @@ __device__ __forceinline__ float stored_to_f32(uint16_t h, bool bf16) {
 template <int F, bool VEC, int KIND>
 __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
     Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
-    const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch, int M, int N,
-    int num_items, int nslices, int remap) {
+    float unscale, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch,
+    int M, int N, int num_items, int nslices, int remap) {
     const int lane = threadIdx.x & (kWave - 1);
     int64_t item_blk;
     int slice;
@@ -224,7 +218,7 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
         static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
     int w, b0, b1, slot;
-    item_range<KIND>(it, item, w, b0, b1, slot);
+    item_range(it, item, w, b0, b1, slot);
     const int col = slice * (64 * F) + lane * F;
     float acc[8][F];
 #pragma unroll
@@ -264,7 +258,7 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
             if (c[v] < 0) break;  // padding sits at the end of the last block
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-                const float a = stored_to_f32(vb[r * 8 + v], bf);
+                const float a = stored_to_f32(vb[r * 8 + v], bf) * unscale;  // exact
 #pragma unroll
                 for (int f = 0; f < F; ++f) acc[r][f] = __builtin_fmaf(a, bv[v][f], acc[r][f]);
             }
@@ -285,14 +279,16 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
 // (tc/ra_segment_hybrid.cu:198-221).
 __global__ __launch_bounds__(kBlock) void tile_merge_kernel(
     const int32_t* __restrict__ split_windows, const int32_t* __restrict__ split_offsets,
-    const float* __restrict__ scratch, float* __restrict__ C, int M, int N) {
+    const int32_t* __restrict__ win_rows, const float* __restrict__ scratch, float* __restrict__ C,
+    int M, int N) {
     const int sw = blockIdx.x;
     const int64_t e = (int64_t)blockIdx.y * kBlock + threadIdx.x;
     if (e >= (int64_t)ra::kTileWindow * N) return;
     const int m = static_cast<int>(e / N);
     const int n = static_cast<int>(e - (int64_t)m * N);
-    const int row = split_windows[sw] * ra::kTileWindow + m;
-    if (row >= M) return;
+    const int64_t slot_row = (int64_t)split_windows[sw] * ra::kTileWindow + m;
+    const int row = win_rows ? win_rows[slot_row] : static_cast<int>(slot_row);
+    if (row < 0 || row >= M) return;
     const int o0 = split_offsets[sw], o1 = split_offsets[sw + 1];
     float acc = scratch[((int64_t)o0 * ra::kTileWindow + m) * N + n];
     for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * ra::kTileWindow + m) * N + n];
@@ -366,7 +362,9 @@ struct ra_tile_plan {
 
 namespace {
 
-// RA_TILE_XCD_REMAP=0 turns the XCD-contiguous window order off.
+// RA_TILE_XCD_REMAP=0 turns the XCD-contiguous window order off.  It is never
+// used for COMMUNITY_TC: the leading-column order clusters the heavy rows at
+// the front, and contiguous ranges would hand all of them to one XCD.
 int tile_remap() {
     static const int r = [] {
         const char* e = std::getenv("RA_TILE_XCD_REMAP");
@@ -405,16 +403,17 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
     int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
     cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
-    const int remap = tile_remap();
+    const int remap = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
+    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
 #define RA_MFMA_CASE(c)                                                                            \
     if (cpl == c) {                                                                                \
         if (bf16)                                                                                  \
             tile_mfma_kernel<c, true, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),    \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale); \
         else                                                                                       \
             tile_mfma_kernel<c, false, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),   \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale); \
     }
     RA_MFMA_CASE(1)
     RA_MFMA_CASE(2)
@@ -433,18 +432,19 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
     const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
     const bool vec = (N % F == 0) && ((reinterpret_cast<uintptr_t>(B) % (4 * F)) == 0);
     const int nslices = (N + 64 * F - 1) / (64 * F);
-    const int remap = tile_remap();
+    const int remap = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
     dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int bf = p->info.value_dtype == RA_DTYPE_BF16;
+    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     const int32_t* ax = p->atox.get<int32_t>();
     const uint16_t* vl = p->vals.get<uint16_t>();
 #define RA_FP32_CASE(f)                                                                              \
     if (F == f) {                                                                                    \
         if (vec)                                                                                     \
-            tile_fp32_kernel<f, true, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, B, C, scratch, M, N, \
+            tile_fp32_kernel<f, true, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch, M, N, \
                                                                    p->num_items, nslices, remap);   \
         else                                                                                         \
-            tile_fp32_kernel<f, false, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, B, C, scratch, M, N, \
+            tile_fp32_kernel<f, false, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch, M, N, \
                                                                     p->num_items, nslices, remap);  \
     }
     RA_FP32_CASE(1)
@@ -458,8 +458,9 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
 ra_status launch_merge(const ra_tile_plan* p, float* C, int N, hipStream_t st) {
     if (p->info.num_split_windows == 0) return RA_OK;
     dim3 grid(p->info.num_split_windows, (8 * N + kBlock - 1) / kBlock);
+    const int32_t* wr = p->info.kind == RA_TILE_COMMUNITY_TC ? p->win_rows.get<int32_t>() : nullptr;
     tile_merge_kernel<<<grid, kBlock, 0, st>>>(p->split_windows.get<int32_t>(),
-                                               p->split_offsets.get<int32_t>(),
+                                               p->split_offsets.get<int32_t>(), wr,
                                                p->scratch.get<float>(), C, p->info.M, N);
     RA_LAUNCH_CHECK("tile_merge_kernel");
     return RA_OK;
@@ -468,7 +469,7 @@ ra_status launch_merge(const ra_tile_plan* p, float* C, int N, hipStream_t st) {
 ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* B32, bool bf16,
                      bool fp32_route, float* C, int N, hipStream_t st) {
     float* scratch = nullptr;
-    if (p->info.kind == RA_TILE_SEGMENT_HYBRID && p->info.num_split_segs > 0) {
+    if (p->info.num_split_segs > 0) {
         RA_TRY(p->scratch.ensure((size_t)p->info.num_split_segs * ra::kTileWindow * N * sizeof(float)));
         scratch = p->scratch.get<float>();
     }
@@ -484,9 +485,9 @@ ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* 
         default:
             RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_SEGMENT_HYBRID>(p, B32, C, scratch, N, st)
                               : launch_mfma_kind<RA_TILE_SEGMENT_HYBRID>(p, Bh, ldb, bf16, C, scratch, N, st));
-            RA_TRY(launch_merge(p, C, N, st));
             break;
     }
+    RA_TRY(launch_merge(p, C, N, st));
     return RA_OK;
 }
 
@@ -531,7 +532,7 @@ ra_status ra_tile_plan_create(int32_t kind, const int32_t* h_rowptr, const int32
             (s = p->seg_slot.upload(host.seg_slot)) == RA_OK &&
             (s = p->split_windows.upload(host.split_windows)) == RA_OK &&
             (s = p->split_offsets.upload(host.split_offsets)) == RA_OK) {
-            p->num_items = kind == RA_TILE_SEGMENT_HYBRID ? p->info.num_segments : p->info.num_windows;
+            p->num_items = p->info.num_segments;
         }
     }
     if (s != RA_OK) {

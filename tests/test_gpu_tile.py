@@ -43,6 +43,7 @@ GRAPHS = {
     "skewed": lambda: S.random_csr(1003, 900, 9.0, seed=3, skew=1.1, empty_frac=0.05),
     "dense_rows": lambda: S.random_csr(200, 3000, 150.0, seed=4),    # > 64 blocks per window
     "community": lambda: S.sbm(64, 50, 12.0, 0.9, seed=6),
+    "hub_windows": lambda: S.random_csr(40, 40000, 2500.0, seed=8),  # > 512 blocks: every kind splits
 }
 
 
@@ -67,8 +68,9 @@ def test_tile_routes(oracle, gname, kind, N):
     assert_close_scaled(C, exact, scale, 2.0 ** -10, "f16 vs exact")
 
     C32 = run(kind, plan, Bd, "fp32", gd).cpu().numpy()
+    qv = oracle.quantize_f16_scaled(g.vals, oracle.tile_value_scale_log2(g.vals))
     seq = oracle.spmm_seq_f32(g.rowptr, g.colind, qv, B)
-    if kind == 2 and plan.num_split_windows > 0:
+    if plan.num_split_windows > 0:
         assert_close_scaled(C32, oracle.spmm_f64(g.rowptr, g.colind, qv, B),
                             oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(B)), 1e-5, "fp32 seg")
     else:
@@ -76,6 +78,22 @@ def test_tile_routes(oracle, gname, kind, N):
 
     # Deterministic across runs.
     np.testing.assert_array_equal(run(kind, plan, Bd, "f16", gd).cpu().numpy(), C)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_tiny_values_keep_fp16_precision(oracle, kind):
+    """GCN-style values far below 1 (hub pairs give 1/sqrt(d_i d_j) ~ 1e-5):
+    the plan's power-of-two value scale keeps them out of the fp16 subnormal
+    range, so the FP16 route stays within 2^-10 of the exact product."""
+    g = S.random_csr(600, 500, 20.0, seed=12)
+    g.vals = (np.abs(g.vals) * 3e-6).astype(np.float32)
+    gd = g.torch("cuda")
+    B = np.random.default_rng(1).standard_normal((g.K, 64)).astype(np.float32)
+    plan = MAKE[kind](gd[0].cpu(), gd[1].cpu(), gd[2].cpu(), g.M, g.K, 64)
+    C = run(kind, plan, torch.from_numpy(B).cuda(), "f16", gd).cpu().numpy()
+    exact = oracle.spmm_f64(g.rowptr, g.colind, g.vals, B)
+    scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B))
+    assert_close_scaled(C, exact, scale, 2.0 ** -10, "tiny values")
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2])

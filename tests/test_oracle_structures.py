@@ -94,8 +94,10 @@ def test_tile_format_matches_oracle(oracle, kind):
         assert np.all(o["atox"][~real] == 0)  # reference pads with column 0
         assert info.num_blocks == o["block_offsets"][-1]
         assert info.num_vectors == int(real.sum())
-        vals = h["vals"].view(np.float16).astype(np.float32).reshape(-1, 8, 8)
-        np.testing.assert_array_equal(vals, oracle.quantize_f16(o["blocks"]))
+        sc = oracle.tile_value_scale_log2(g.vals)
+        assert info.value_scale_log2 == sc
+        vals = h["vals"].view(np.float16).astype(np.float32).reshape(-1, 8, 8) * np.float32(2.0 ** -sc)
+        np.testing.assert_array_equal(vals, oracle.quantize_f16_scaled(o["blocks"], sc))
         if kind == 2:
             for key in ("seg_bbegin", "seg_bend", "seg_slot", "split_windows", "split_offsets"):
                 np.testing.assert_array_equal(h[key], o[key], err_msg=key)
@@ -138,18 +140,62 @@ def test_value_rounding_matches_numpy(oracle):
     x = x[np.abs(x) < 1e30]
     M = len(x)
     g = S.Graph(np.arange(M + 1, dtype=np.int32), np.zeros(M, np.int32), x, M, 1)
-    for vd, q in ((capi.DTYPE_F16, oracle.quantize_f16), (capi.DTYPE_BF16, oracle.quantize_bf16)):
-        _, h = tile_host(0, g, value_dtype=vd)
-        blocks = h["vals"].reshape(-1, 8, 8)[:, :, 0].reshape(-1)[:M]
-        if vd == capi.DTYPE_F16:
-            got = blocks.view(np.float16).astype(np.float32)
-        else:
-            got = (blocks.astype(np.uint32) << 16).view(np.float32)
-        with np.errstate(over="ignore"):
-            np.testing.assert_array_equal(got, q(x))
+    # bf16 plans are never scaled: the raw RNE conversion over the full range.
+    _, h = tile_host(0, g, value_dtype=capi.DTYPE_BF16)
+    blocks = h["vals"].reshape(-1, 8, 8)[:, :, 0].reshape(-1)[:M]
+    got = (blocks.astype(np.uint32) << 16).view(np.float32)
+    np.testing.assert_array_equal(got, oracle.quantize_bf16(x))
+    # fp16 plans scale max|v| into [2^13, 2^14); with max|v| = 10000 the scale
+    # is 2^0, so the raw RNE conversion is pinned on everything below it,
+    # including the fp16 subnormal range.  (Values near the fp16 maximum are
+    # unreachable through a plan by construction.)
+    x0 = np.clip(x, -9000.0, 9000.0).astype(np.float32)
+    x0[0] = 10000.0
+    g0 = S.Graph(np.arange(M + 1, dtype=np.int32), np.zeros(M, np.int32), x0, M, 1)
+    info, h = tile_host(0, g0, value_dtype=capi.DTYPE_F16)
+    assert info.value_scale_log2 == 0
+    blocks = h["vals"].reshape(-1, 8, 8)[:, :, 0].reshape(-1)[:M]
+    np.testing.assert_array_equal(blocks.view(np.float16).astype(np.float32), oracle.quantize_f16(x0))
+
+
+def test_value_scale_closed_form(oracle):
+    """max|v| = 2^e maps to s = 13 - e; GCN-like tiny values keep fp16 precision."""
+    for e in (-20, -5, 0, 3, 13, 14, 30):
+        v = np.array([2.0 ** e, -(2.0 ** (e - 3))], np.float32)
+        g = S.Graph(np.array([0, 2], np.int32), np.array([0, 1], np.int32), v, 1, 2)
+        info, h = tile_host(0, g)
+        assert info.value_scale_log2 == oracle.tile_value_scale_log2(v) == max(-24, min(24, 13 - e))
+    tiny = np.array([3.3e-5, 1.0 / 3.0, 2.5e-6], np.float32)
+    sc = oracle.tile_value_scale_log2(tiny)
+    rel = np.abs(oracle.quantize_f16_scaled(tiny, sc) - tiny) / tiny
+    assert np.all(rel <= 2.0 ** -11)
 
 
 def test_inactive_below_n16():
     g = S.random_csr(20, 20, 3.0, seed=0)
     info, _ = tile_host(0, g, N=8)
     assert info.active == 0
+
+
+@pytest.mark.parametrize("kind,limit", [(0, 512), (1, 512), (2, 64)])
+def test_segments_cover_windows(kind, limit):
+    """Every kind is scheduled as segments: each window's block range is cut
+    into consecutive pieces of at most `limit` blocks (64 for SEGMENT_HYBRID as
+    in tc/ra_segment_hybrid.cu:470-498; 512 for the other two), sole windows
+    flagged in bit 31, partial slots numbered in ascending order."""
+    g = S.random_csr(40, 40000, 2500.0, seed=8)
+    info, h = tile_host(kind, g)
+    bo = h["block_offsets"]
+    segw = h["seg_window"].view(np.uint32)
+    covered = {}
+    for w_tag, b0, b1, slot in zip(segw, h["seg_bbegin"], h["seg_bend"], h["seg_slot"]):
+        w = int(w_tag & 0x7FFFFFFF)
+        assert 0 < b1 - b0 <= limit or bo[w + 1] == bo[w]
+        assert bool(w_tag & 0x80000000) == (bo[w + 1] - bo[w] <= limit)
+        covered.setdefault(w, []).append((int(b0), int(b1)))
+    for w, pieces in covered.items():
+        pieces.sort()
+        assert pieces[0][0] == bo[w] and pieces[-1][1] == bo[w + 1]
+        assert all(a[1] == b[0] for a, b in zip(pieces, pieces[1:]))
+    assert info.num_split_windows == len(h["split_windows"]) > 0
+    assert h["split_offsets"][-1] == info.num_split_segs
