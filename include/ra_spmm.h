@@ -266,6 +266,16 @@ void ra_tile_host_destroy(ra_tile_host* host);
 ra_status ra_tile_plan_create(int32_t kind, const int32_t* h_rowptr, const int32_t* h_colind,
                               const float* h_vals, int32_t M, int32_t K, int32_t N,
                               int32_t value_dtype, ra_tile_plan** out);
+/* Device build of the same format (sorts and scans on the GPU; the cold-path
+ * replacement of the reference's host OpenMP build).  CSR arrays are device
+ * pointers; synchronises `stream`.  The result is bit-identical to
+ * ra_tile_plan_create on the same input. */
+ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, const int32_t* d_colind,
+                                     const float* d_vals, int32_t M, int32_t K, int32_t N,
+                                     int32_t value_dtype, ra_stream_t stream, ra_tile_plan** out);
+/* Copy a plan array back to the host (same names as ra_tile_host_export). */
+ra_status ra_tile_plan_export(const ra_tile_plan* plan, const char* name, void* dst,
+                              int64_t* count);
 /* B fp32 [K,N]; route: ra_tile_route.  The FP16/BF16 routes convert B into
  * plan scratch first (one extra pass over B). */
 ra_status ra_tile_plan_run(ra_tile_plan* plan, const float* d_B, float* d_C, int32_t N,

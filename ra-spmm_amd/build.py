@@ -37,6 +37,7 @@ SOURCES = {
     "tile_build.cpp": [],
     "csr_kernels.hip": [],
     "tile_kernels.hip": [],
+    "tile_build_gpu.hip": [],
 }
 LIB_NAME = "libra_spmm_hip.so"
 

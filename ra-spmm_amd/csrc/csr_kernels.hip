@@ -381,10 +381,13 @@ struct LaneShape {
 // width (4..64), RA_CSR_UNROLL the gathers in flight per lane (4 or 8),
 // RA_XCD_REMAP=0 turns the XCD-contiguous block order of CSR_DIRECT off
 // (RA_ZO_XCD_REMAP=1 turns it on for ZERO_OVERHEAD_CSR, where it piles the hub
-// chunks onto one XCD), RA_CSR_STREAMING=0 turns the non-temporal hints off.
+// chunks onto one XCD), RA_CSR_STREAMING=0 turns the non-temporal hints off,
+// RA_CSR_COLTILE=c processes the columns in passes of c elements (the grid's
+// slowest dimension), so each pass gathers only a c-column slice of B.
 struct CsrTuning {
-    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1;
+    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0;
     CsrTuning() {
+        if (const char* e = std::getenv("RA_CSR_COLTILE")) coltile = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_LANES")) lanes = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_UNROLL")) unroll = std::atoi(e) >= 8 ? 8 : 4;
         if (const char* e = std::getenv("RA_XCD_REMAP")) remap = std::atoi(e) != 0;
@@ -397,9 +400,10 @@ const CsrTuning& tuning() {
     return t;
 }
 
-// Lane-group shape from the number of packets per row.
-LaneShape pick_shape(int np) {
+// Lane-group shape from the number of packets per row (per column pass).
+LaneShape pick_shape(int np, int packet_elems) {
     const CsrTuning& t = tuning();
+    if (t.coltile > 0) np = std::min(np, std::max(1, t.coltile / packet_elems));
     int G;
     if (t.lanes >= 4 && t.lanes <= 64 && (t.lanes & (t.lanes - 1)) == 0) G = t.lanes;
     else G = np <= 4 ? 4 : np <= 8 ? 8 : np <= 16 ? 16 : np <= 32 ? 32 : 64;
@@ -501,7 +505,7 @@ ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
     const int np = vec ? N / 4 : N;
-    const LaneShape sh = pick_shape(np);
+    const LaneShape sh = pick_shape(np, vec ? 4 : 1);
     const int rows_per_block = kWavesPerBlock * (kWave / sh.G);
     dim3 grid((M + rows_per_block - 1) / rows_per_block, (np + sh.G * sh.V - 1) / (sh.G * sh.V));
     if (vec)
@@ -680,7 +684,7 @@ ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
     const int np = vec ? N / 4 : N;
-    const LaneShape sh = pick_shape(np);
+    const LaneShape sh = pick_shape(np, vec ? 4 : 1);
     if (plan->info.num_split_chunks > 0)
         RA_TRY(plan->partials.ensure((size_t)plan->info.num_split_chunks * N * sizeof(float)));
     const int RPW = kWave / sh.G;

@@ -1,0 +1,468 @@
+// tile_build_gpu.hip — device build of the tile format (cold path).
+//
+// Same windows, vectors, blocks, value rounding and segment tables as the host
+// builder (tile_build.cpp), produced with sorts and scans on the GPU:
+//   1. (COMMUNITY_TC) rows sorted by (leading column or INT_MAX, row) -> window slots
+//   2. one 64-bit key per nonzero: (window << 34) | (column << 3) | slot
+//   3. stable radix sort of (key, CSR position)  -> per-window (col, slot) order,
+//      duplicates adjacent in CSR order
+//   4. scans: vector ids, vectors and blocks per window, block offsets
+//   5. scatter: atox (first entry of each vector), values (first entry of each
+//      (col, slot) sums its duplicates in CSR order, scales, rounds)
+//   6. segment tables of the split schedule (64 blocks for SEGMENT_HYBRID,
+//      kTileDirectSplitBlocks otherwise)
+// Reference algorithm: tc/ra_tc_direct.cu:654-706, tc/ra_community_tc.cu:335-403,
+// tc/ra_segment_hybrid.cu:470-498 (the reference builds on the host with OpenMP).
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <chrono>
+#include <climits>
+#include <cmath>
+#include <cstring>
+
+#include "half_convert.hpp"
+#include "ra_internal.hpp"
+#include "tile_format.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+unsigned grid_for(int64_t n) {
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, 1 << 20)));
+}
+
+#define RA_GRID_STRIDE(i, n) \
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (n); i += (int64_t)gridDim.x * blockDim.x)
+
+__global__ void fill_i32(int32_t* p, int64_t n, int32_t v) { RA_GRID_STRIDE(i, n) p[i] = v; }
+__global__ void fill_u16(uint16_t* p, int64_t n) { RA_GRID_STRIDE(i, n) p[i] = 0; }
+__global__ void fill_u32(unsigned* p, int64_t n) { RA_GRID_STRIDE(i, n) p[i] = 0u; }
+
+// Validity counters: [0] rows with rowptr[r+1] < rowptr[r], [1] columns outside [0, K).
+__global__ void validate_csr(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
+                             int M, int K, int64_t base, int64_t n, unsigned* __restrict__ bad) {
+    RA_GRID_STRIDE(r, (int64_t)M) {
+        if (rowptr[r + 1] < rowptr[r]) atomicAdd(&bad[0], 1u);
+    }
+    RA_GRID_STRIDE(t, n) {
+        const int c = colind[base + t];
+        if (c < 0 || c >= K) atomicAdd(&bad[1], 1u);
+    }
+}
+
+// max |v| as the bit pattern of a non-negative float (monotone as unsigned).
+__global__ void abs_max_bits(const float* __restrict__ vals, int64_t base, int64_t n,
+                             unsigned* __restrict__ out) {
+    unsigned m = 0;
+    RA_GRID_STRIDE(t, n) {
+        const unsigned b = ra::float_bits(vals[base + t]) & 0x7FFFFFFFu;
+        if (b <= 0x7F800000u) m = max(m, b);  // ignore NaN payloads
+    }
+    for (int off = 32; off > 0; off >>= 1) m = max(m, __shfl_xor(m, off, 64));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+
+__global__ void lead_keys(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind, int M,
+                          uint64_t* __restrict__ keys) {
+    RA_GRID_STRIDE(r, (int64_t)M) {
+        const uint32_t lead = rowptr[r] < rowptr[r + 1] ? static_cast<uint32_t>(colind[rowptr[r]])
+                                                        : static_cast<uint32_t>(INT_MAX);
+        keys[r] = (static_cast<uint64_t>(lead) << 32) | static_cast<uint32_t>(r);
+    }
+}
+
+__global__ void place_rows(const uint64_t* __restrict__ sorted, int M, int64_t slots,
+                           int32_t* __restrict__ win_rows, int32_t* __restrict__ pos) {
+    RA_GRID_STRIDE(i, slots) {
+        if (i < M) {
+            const int32_t row = static_cast<int32_t>(sorted[i] & 0xFFFFFFFFu);
+            win_rows[i] = row;
+            pos[row] = static_cast<int32_t>(i);
+        } else {
+            win_rows[i] = -1;
+        }
+    }
+}
+
+__global__ void identity_rows(int M, int64_t slots, int32_t* __restrict__ win_rows) {
+    RA_GRID_STRIDE(i, slots) win_rows[i] = i < M ? static_cast<int32_t>(i) : -1;
+}
+
+// Key of every nonzero; the row of position p is found by binary search.
+__global__ void entry_keys(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
+                           const int32_t* __restrict__ pos, int M, int64_t base, int64_t n,
+                           uint64_t* __restrict__ keys, int32_t* __restrict__ idx) {
+    RA_GRID_STRIDE(t, n) {
+        const int64_t p = base + t;
+        int lo = 0, hi = M - 1;  // last row with rowptr[row] <= p
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (rowptr[mid] <= p) lo = mid;
+            else hi = mid - 1;
+        }
+        const int64_t slot_pos = pos ? pos[lo] : lo;
+        keys[t] = (static_cast<uint64_t>(slot_pos >> 3) << 34) |
+                  (static_cast<uint64_t>(static_cast<uint32_t>(colind[p])) << 3) |
+                  static_cast<uint64_t>(slot_pos & 7);
+        idx[t] = static_cast<int32_t>(t);
+    }
+}
+
+__global__ void mark_new(const uint64_t* __restrict__ keys, int64_t n, int32_t* __restrict__ newvec,
+                         int32_t* __restrict__ newkey) {
+    RA_GRID_STRIDE(i, n) {
+        const uint64_t k = keys[i];
+        const bool first = i == 0;
+        const uint64_t prev = first ? 0 : keys[i - 1];
+        newvec[i] = (first || (k >> 3) != (prev >> 3)) ? 1 : 0;
+        newkey[i] = (first || k != prev) ? 1 : 0;
+    }
+}
+
+__global__ void count_vectors(const uint64_t* __restrict__ keys, const int32_t* __restrict__ newvec,
+                              int64_t n, int32_t* __restrict__ nvec) {
+    RA_GRID_STRIDE(i, n) {
+        if (newvec[i]) atomicAdd(&nvec[keys[i] >> 34], 1);
+    }
+}
+
+__global__ void window_counts(const int32_t* __restrict__ nvec, int W, int limit,
+                              int32_t* __restrict__ blocks, int32_t* __restrict__ segs,
+                              int32_t* __restrict__ split_slots, int32_t* __restrict__ is_split) {
+    RA_GRID_STRIDE(w, (int64_t)W) {
+        const int b = (nvec[w] + ra::kTileVec - 1) / ra::kTileVec;
+        blocks[w] = b;
+        const bool split = b > limit;
+        const int ns = split ? (b + limit - 1) / limit : 1;
+        segs[w] = ns;
+        split_slots[w] = split ? ns : 0;
+        is_split[w] = split ? 1 : 0;
+    }
+}
+
+__global__ void scatter_entries(const uint64_t* __restrict__ keys, const int32_t* __restrict__ idx,
+                                const int32_t* __restrict__ vid, const int32_t* __restrict__ newkey,
+                                int64_t n, const float* __restrict__ vals, int64_t base,
+                                const int32_t* __restrict__ block_offsets,
+                                const int32_t* __restrict__ win_vec_start, float vscale, int bf16,
+                                int32_t* __restrict__ atox, uint16_t* __restrict__ out) {
+    RA_GRID_STRIDE(i, n) {
+        if (!newkey[i]) continue;
+        const uint64_t k = keys[i];
+        const int64_t w = static_cast<int64_t>(k >> 34);
+        const int32_t col = static_cast<int32_t>((k >> 3) & 0x7FFFFFFFu);
+        const int slot = static_cast<int>(k & 7u);
+        const int64_t vlocal = (int64_t)(vid[i] - 1) - win_vec_start[w];
+        const int64_t blk = block_offsets[w] + vlocal / ra::kTileVec;
+        const int kk = static_cast<int>(vlocal % ra::kTileVec);
+        atox[blk * ra::kTileVec + kk] = col;
+        // Duplicates of (window, col, slot) follow in CSR order (stable sort).
+        float acc = 0.f + vals[base + idx[i]];
+        for (int64_t j = i + 1; j < n && keys[j] == k; ++j) acc += vals[base + idx[j]];
+        out[blk * 64 + slot * ra::kTileVec + kk] =
+            bf16 ? ra::bf16_rne_bits(acc) : ra::half_rne_bits(acc * vscale);
+    }
+}
+
+__global__ void fill_segments(const int32_t* __restrict__ block_offsets, const int32_t* __restrict__ seg_start,
+                              const int32_t* __restrict__ slot_start, const int32_t* __restrict__ split_idx,
+                              int W, int limit, int32_t* __restrict__ seg_window,
+                              int32_t* __restrict__ seg_bbegin, int32_t* __restrict__ seg_bend,
+                              int32_t* __restrict__ seg_slot, int32_t* __restrict__ split_windows,
+                              int32_t* __restrict__ split_offsets) {
+    RA_GRID_STRIDE(w, (int64_t)W) {
+        const int b0 = block_offsets[w], b1 = block_offsets[w + 1];
+        const int s0 = seg_start[w];
+        if (b1 - b0 <= limit) {
+            seg_window[s0] = static_cast<int32_t>(static_cast<uint32_t>(w) | ra::kTileSoleFlag);
+            seg_bbegin[s0] = b0;
+            seg_bend[s0] = b1;
+            seg_slot[s0] = -1;
+        } else {
+            int t = 0;
+            for (int b = b0; b < b1; b += limit, ++t) {
+                seg_window[s0 + t] = static_cast<int32_t>(w);
+                seg_bbegin[s0 + t] = b;
+                seg_bend[s0 + t] = min(b + limit, b1);
+                seg_slot[s0 + t] = slot_start[w] + t;
+            }
+            const int j = split_idx[w];
+            split_windows[j] = static_cast<int32_t>(w);
+            split_offsets[j + 1] = slot_start[w] + t;
+        }
+        if (w == 0) split_offsets[0] = 0;
+    }
+}
+
+struct Scratch {
+    ra::DeviceBuffer buf;
+    template <typename T>
+    T* take(size_t count, size_t& off) {
+        off = (off + 255) & ~size_t(255);
+        T* p = reinterpret_cast<T*>(buf.get<char>() + off);
+        off += count * sizeof(T);
+        return p;
+    }
+};
+
+template <typename T>
+ra_status read_back(T* dst, const T* src, size_t n, hipStream_t st) {
+    RA_HIP_TRY(hipMemcpyAsync(dst, src, n * sizeof(T), hipMemcpyDeviceToHost, st));
+    RA_HIP_TRY(hipStreamSynchronize(st));
+    return RA_OK;
+}
+
+ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const int32_t* colind,
+                    const float* vals, int32_t M, int32_t K, int32_t N, int32_t value_dtype, hipStream_t st) {
+    p->info = ra_tile_info{};
+    p->info.kind = kind;
+    p->info.M = M;
+    p->info.K = K;
+    p->info.value_dtype = value_dtype;
+    if (M == 0 || K == 0 || N < 16) return RA_OK;  // inactive, like the host build
+    int32_t ends[2];
+    RA_TRY(read_back(&ends[0], rowptr, 1, st));
+    RA_TRY(read_back(&ends[1], rowptr + M, 1, st));
+    const int64_t base = ends[0];
+    const int64_t n = static_cast<int64_t>(ends[1]) - ends[0];
+    if (n < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rowptr not monotone");
+    if (n > INT32_MAX) return ra::fail(RA_ERR_UNSUPPORTED, "tile: more than 2^31-1 nonzeros");
+    const int64_t W = (M + ra::kTileWindow - 1) / ra::kTileWindow;
+    const int64_t slots = W * ra::kTileWindow;
+    const int limit = kind == RA_TILE_SEGMENT_HYBRID ? ra::kTileSegBlocks : ra::kTileDirectSplitBlocks;
+    const bool bf16 = value_dtype == RA_DTYPE_BF16;
+    const int64_t nn = std::max<int64_t>(n, 1);
+
+    // Temporary storage for the sorts and scans, sized by a dry run.
+    size_t sort_bytes = 0, scan_bytes = 0, red_bytes = 0;
+    uint64_t* knull = nullptr;
+    int32_t* inull = nullptr;
+    RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, knull, knull, inull, inull,
+                                                  static_cast<int>(std::max<int64_t>(nn, M)), 0, 64, st));
+    RA_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, inull, inull, static_cast<int>(nn), st));
+    size_t scan2 = 0;
+    RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, scan2, inull, inull, static_cast<int>(W + 1), st));
+    scan_bytes = std::max(scan_bytes, scan2);
+    RA_HIP_TRY(hipcub::DeviceReduce::Max(nullptr, red_bytes, inull, inull, static_cast<int>(W), st));
+    size_t red2 = 0;
+    RA_HIP_TRY(hipcub::DeviceReduce::Sum(nullptr, red2, inull, inull, static_cast<int>(nn), st));
+    red_bytes = std::max(red_bytes, red2);
+    const size_t tmp_bytes = std::max({sort_bytes, scan_bytes, red_bytes});
+
+    const size_t need = 256 * 24 + tmp_bytes + nn * (2 * 8 + 2 * 4 + 3 * 4) +
+                        std::max<int64_t>(M, 1) * (2 * 8 + 4) + (W + 1) * 4 * 9 + 64;
+    Scratch s;
+    RA_TRY(s.buf.allocate(need));
+    size_t off = 0;
+    void* tmp = s.take<char>(tmp_bytes, off);
+    uint64_t* keys = s.take<uint64_t>(nn, off);
+    uint64_t* keys2 = s.take<uint64_t>(nn, off);
+    int32_t* idx = s.take<int32_t>(nn, off);
+    int32_t* idx2 = s.take<int32_t>(nn, off);
+    int32_t* newvec = s.take<int32_t>(nn, off);
+    int32_t* newkey = s.take<int32_t>(nn, off);
+    int32_t* vid = s.take<int32_t>(nn, off);
+    uint64_t* rkeys = s.take<uint64_t>(std::max<int64_t>(M, 1), off);
+    uint64_t* rkeys2 = s.take<uint64_t>(std::max<int64_t>(M, 1), off);
+    int32_t* pos = s.take<int32_t>(std::max<int64_t>(M, 1), off);
+    int32_t* nvec = s.take<int32_t>(W + 1, off);
+    int32_t* wvec_start = s.take<int32_t>(W + 1, off);
+    int32_t* blocks = s.take<int32_t>(W + 1, off);
+    int32_t* segs = s.take<int32_t>(W + 1, off);
+    int32_t* seg_start = s.take<int32_t>(W + 1, off);
+    int32_t* split_slots = s.take<int32_t>(W + 1, off);
+    int32_t* slot_start = s.take<int32_t>(W + 1, off);
+    int32_t* is_split = s.take<int32_t>(W + 1, off);
+    int32_t* split_idx = s.take<int32_t>(W + 1, off);
+    unsigned* flags = s.take<unsigned>(4, off);
+    int32_t* red_out = s.take<int32_t>(2, off);
+
+    // Validation and value scale.
+    fill_u32<<<1, kThreads, 0, st>>>(flags, 4);
+    validate_csr<<<grid_for(std::max<int64_t>(M, n)), kThreads, 0, st>>>(rowptr, colind, M, K, base, n, flags);
+    abs_max_bits<<<grid_for(n), kThreads, 0, st>>>(vals, base, n, flags + 2);
+    RA_LAUNCH_CHECK("validate_csr");
+    unsigned hflags[4];
+    RA_TRY(read_back(hflags, flags, 4, st));
+    if (hflags[0]) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rowptr not monotone");
+    if (hflags[1]) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: column index out of range");
+    float vmax;
+    std::memcpy(&vmax, &hflags[2], 4);
+    p->info.value_scale_log2 = bf16 ? 0 : ra::f16_value_scale_log2(vmax);
+    const float vscale = std::ldexp(1.0f, p->info.value_scale_log2);
+
+    // Row -> window slot.
+    RA_TRY(p->win_rows.allocate(slots * sizeof(int32_t)));
+    const int32_t* pos_ptr = nullptr;
+    if (kind == RA_TILE_COMMUNITY_TC) {
+        lead_keys<<<grid_for(M), kThreads, 0, st>>>(rowptr, colind, M, rkeys);
+        // Keys are unique, so the radix sort yields the stable leading-column order.
+        size_t tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, rkeys, rkeys2, M, 0, 63, st));
+        place_rows<<<grid_for(slots), kThreads, 0, st>>>(rkeys2, M, slots, p->win_rows.get<int32_t>(), pos);
+        pos_ptr = pos;
+    } else {
+        identity_rows<<<grid_for(slots), kThreads, 0, st>>>(M, slots, p->win_rows.get<int32_t>());
+    }
+    RA_LAUNCH_CHECK("window slots");
+
+    // Sort nonzeros by (window, column, slot), stable in CSR position.
+    int wbits = 0;
+    while ((int64_t(1) << wbits) < W) ++wbits;
+    if (n > 0) {
+        entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, keys, idx);
+        size_t tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, keys2, idx, idx2, static_cast<int>(n),
+                                                      0, 34 + wbits, st));
+        mark_new<<<grid_for(n), kThreads, 0, st>>>(keys2, n, newvec, newkey);
+        tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tb, newvec, vid, static_cast<int>(n), st));
+    }
+    fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(nvec, W + 1, 0);
+    if (n > 0) count_vectors<<<grid_for(n), kThreads, 0, st>>>(keys2, newvec, n, nvec);
+    window_counts<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), limit, blocks, segs,
+                                                    split_slots, is_split);
+    fill_i32<<<1, kThreads, 0, st>>>(blocks + W, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(segs + W, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(split_slots + W, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(is_split + W, 1, 0);
+    RA_LAUNCH_CHECK("window counts");
+    RA_TRY(p->block_offsets.allocate((W + 1) * sizeof(int32_t)));
+    int32_t* boff = p->block_offsets.get<int32_t>();
+    {
+        size_t tb = tmp_bytes;
+        const int wn = static_cast<int>(W + 1);
+        RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, nvec, wvec_start, wn, st));
+        tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, blocks, boff, wn, st));
+        tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, segs, seg_start, wn, st));
+        tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, split_slots, slot_start, wn, st));
+        tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, is_split, split_idx, wn, st));
+        tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceReduce::Max(tmp, tb, blocks, red_out, static_cast<int>(W), st));
+        if (n > 0) {
+            tb = tmp_bytes;
+            RA_HIP_TRY(hipcub::DeviceReduce::Sum(tmp, tb, newkey, red_out + 1, static_cast<int>(n), st));
+        } else {
+            fill_i32<<<1, kThreads, 0, st>>>(red_out + 1, 1, 0);
+        }
+    }
+    int32_t totals[6];  // blocks, vectors, segments, slots, split windows
+    RA_TRY(read_back(&totals[0], boff + W, 1, st));
+    RA_TRY(read_back(&totals[1], wvec_start + W, 1, st));
+    RA_TRY(read_back(&totals[2], seg_start + W, 1, st));
+    RA_TRY(read_back(&totals[3], slot_start + W, 1, st));
+    RA_TRY(read_back(&totals[4], split_idx + W, 1, st));
+    int32_t reds[2];
+    RA_TRY(read_back(reds, red_out, 2, st));
+    const int64_t nblocks = totals[0];
+    if (nblocks > INT32_MAX / 64) return ra::fail(RA_ERR_UNSUPPORTED, "tile: too many blocks for int32 offsets");
+
+    // atox, values.
+    RA_TRY(p->atox.allocate(std::max<int64_t>(nblocks, 1) * ra::kTileVec * sizeof(int32_t)));
+    RA_TRY(p->vals.allocate(std::max<int64_t>(nblocks, 1) * 64 * sizeof(uint16_t)));
+    fill_i32<<<grid_for(nblocks * ra::kTileVec), kThreads, 0, st>>>(p->atox.get<int32_t>(), nblocks * ra::kTileVec, -1);
+    fill_u16<<<grid_for(nblocks * 64), kThreads, 0, st>>>(p->vals.get<uint16_t>(), nblocks * 64);
+    if (n > 0)
+        scatter_entries<<<grid_for(n), kThreads, 0, st>>>(keys2, idx2, vid, newkey, n, vals, base, boff,
+                                                          wvec_start, vscale, bf16 ? 1 : 0,
+                                                          p->atox.get<int32_t>(), p->vals.get<uint16_t>());
+    RA_LAUNCH_CHECK("scatter_entries");
+
+    // Segment tables.
+    const int64_t nseg = totals[2], nsplit = totals[4];
+    RA_TRY(p->seg_window.allocate(nseg * sizeof(int32_t)));
+    RA_TRY(p->seg_bbegin.allocate(nseg * sizeof(int32_t)));
+    RA_TRY(p->seg_bend.allocate(nseg * sizeof(int32_t)));
+    RA_TRY(p->seg_slot.allocate(nseg * sizeof(int32_t)));
+    RA_TRY(p->split_windows.allocate(std::max<int64_t>(nsplit, 1) * sizeof(int32_t)));
+    RA_TRY(p->split_offsets.allocate((nsplit + 1) * sizeof(int32_t)));
+    fill_segments<<<grid_for(W), kThreads, 0, st>>>(boff, seg_start, slot_start, split_idx, static_cast<int>(W),
+                                                    limit, p->seg_window.get<int32_t>(), p->seg_bbegin.get<int32_t>(),
+                                                    p->seg_bend.get<int32_t>(), p->seg_slot.get<int32_t>(),
+                                                    p->split_windows.get<int32_t>(), p->split_offsets.get<int32_t>());
+    RA_LAUNCH_CHECK("fill_segments");
+    RA_HIP_TRY(hipStreamSynchronize(st));
+
+    ra_tile_info& I = p->info;
+    I.active = 1;
+    I.num_windows = static_cast<int32_t>(W);
+    I.num_blocks = static_cast<int32_t>(nblocks);
+    I.num_segments = static_cast<int32_t>(nseg);
+    I.num_split_windows = static_cast<int32_t>(nsplit);
+    I.num_split_segs = totals[3];
+    I.max_window_blocks = reds[0];
+    I.nnz = reds[1];
+    I.num_vectors = totals[1];
+    I.avg_tile_density = nblocks > 0 ? static_cast<float>(static_cast<double>(I.nnz) / (64.0 * nblocks)) : 0.f;
+    I.plan_bytes = static_cast<int64_t>(4 * (slots + (W + 1) + nblocks * ra::kTileVec + 4 * nseg + nsplit +
+                                             nsplit + 1) +
+                                        2 * nblocks * 64);
+    p->num_items = static_cast<int32_t>(nseg);
+    return RA_OK;
+}
+
+const ra::DeviceBuffer* plan_array(const ra_tile_plan* p, const std::string& n, size_t& elem, int64_t& count) {
+    const ra_tile_info& I = p->info;
+    const int64_t W = I.num_windows;
+    elem = 4;
+    if (n == "block_offsets") { count = I.active ? W + 1 : 0; return &p->block_offsets; }
+    if (n == "atox") { count = (int64_t)I.num_blocks * ra::kTileVec; return &p->atox; }
+    if (n == "win_rows") { count = W * ra::kTileWindow; return &p->win_rows; }
+    if (n == "vals") { elem = 2; count = (int64_t)I.num_blocks * 64; return &p->vals; }
+    if (n == "seg_window") { count = I.num_segments; return &p->seg_window; }
+    if (n == "seg_bbegin") { count = I.num_segments; return &p->seg_bbegin; }
+    if (n == "seg_bend") { count = I.num_segments; return &p->seg_bend; }
+    if (n == "seg_slot") { count = I.num_segments; return &p->seg_slot; }
+    if (n == "split_windows") { count = I.num_split_windows; return &p->split_windows; }
+    if (n == "split_offsets") { count = I.active ? I.num_split_windows + 1 : 0; return &p->split_offsets; }
+    return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, const int32_t* d_colind,
+                                     const float* d_vals, int32_t M, int32_t K, int32_t N,
+                                     int32_t value_dtype, ra_stream_t stream, ra_tile_plan** out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: out is NULL");
+    *out = nullptr;
+    if (kind < RA_TILE_TC_DIRECT || kind > RA_TILE_SEGMENT_HYBRID)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: unknown kind");
+    if (value_dtype != RA_DTYPE_F16 && value_dtype != RA_DTYPE_BF16)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: value_dtype must be F16 or BF16");
+    if (M < 0 || K < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: negative dimension");
+    if (M > 0 && (!d_rowptr || !d_colind || !d_vals))
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: NULL CSR array");
+    const auto t0 = std::chrono::steady_clock::now();
+    auto p = new (std::nothrow) ra_tile_plan();
+    if (!p) return ra::fail(RA_ERR_OUT_OF_MEMORY, "tile: plan allocation");
+    const ra_status s = gpu_build(p, kind, d_rowptr, d_colind, d_vals, M, K, N, value_dtype,
+                                  reinterpret_cast<hipStream_t>(stream));
+    if (s != RA_OK) {
+        delete p;
+        return s;
+    }
+    p->info.build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    *out = p;
+    return RA_OK;
+}
+
+ra_status ra_tile_plan_export(const ra_tile_plan* p, const char* name, void* dst, int64_t* count) {
+    if (!p || !name || !count) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile export: NULL argument");
+    size_t elem = 4;
+    int64_t n = 0;
+    const ra::DeviceBuffer* b = plan_array(p, name, elem, n);
+    if (!b) return ra::fail(RA_ERR_INVALID_ARGUMENT, std::string("tile export: unknown array '") + name + "'");
+    *count = n;
+    if (dst && n > 0) RA_HIP_TRY(hipMemcpy(dst, b->get(), n * elem, hipMemcpyDeviceToHost));
+    return RA_OK;
+}
+
+}  // extern "C"

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../include/ra_spmm.h"
+#include "ra_internal.hpp"
 
 struct ra_tile_host {
     int32_t kind = 0, M = 0, K = 0, N = 0, value_dtype = RA_DTYPE_F16;
@@ -56,3 +57,13 @@ ra_status tile_host_build(int32_t kind, const int32_t* rowptr, const int32_t* co
                           ra_tile_host& out);
 
 }  // namespace ra
+
+// Device plan: the same arrays in HBM plus per-plan scratch.
+struct ra_tile_plan {
+    ra_tile_info info{};
+    int32_t num_items = 0;  // segments (every kind is scheduled as segments)
+    ra::DeviceBuffer block_offsets, atox, vals, win_rows, seg_window, seg_bbegin, seg_bend,
+        seg_slot, split_windows, split_offsets;
+    ra::DeviceBuffer bconv;    // B converted to fp16/bf16 (grown per K*ldb)
+    ra::DeviceBuffer scratch;  // partial slots of split windows
+};

@@ -350,16 +350,6 @@ ra_status launch_convert(const float* in, void* out, int64_t rows, int32_t cols,
 
 }  // namespace
 
-// ============================================================ plan object
-struct ra_tile_plan {
-    ra_tile_info info{};
-    int32_t num_items = 0;
-    ra::DeviceBuffer block_offsets, atox, vals, win_rows, seg_window, seg_bbegin, seg_bend,
-        seg_slot, split_windows, split_offsets;
-    ra::DeviceBuffer bconv;    // B converted to fp16/bf16 (grown per K*ldb)
-    ra::DeviceBuffer scratch;  // SEGMENT_HYBRID partial slots
-};
-
 namespace {
 
 // RA_TILE_XCD_REMAP=0 turns the XCD-contiguous window order off.  It is never

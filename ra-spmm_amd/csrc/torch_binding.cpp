@@ -316,18 +316,36 @@ int parse_value_dtype(const std::string& s) {
     return -1;
 }
 
+// build: "auto" (device build; host tensors are uploaded first), "gpu", or
+// "host" (the host C++ builder).  Both produce the same plan bit for bit.
 std::shared_ptr<TilePlan> make_tile_plan(int kind, torch::Tensor rowptr_cpu, torch::Tensor colind_cpu,
                                          torch::Tensor vals_cpu, int M, int K, int N,
-                                         const std::string& value_dtype, const char* what) {
-    auto rp = host_i32(rowptr_cpu);
-    auto ci = host_i32(colind_cpu);
-    auto vl = host_f32(vals_cpu);
-    TORCH_CHECK(rp.numel() >= M + 1, "rowptr has fewer than M+1 entries");
+                                         const std::string& value_dtype, const std::string& build,
+                                         const char* what) {
+    TORCH_CHECK(build == "auto" || build == "gpu" || build == "host",
+                "build must be 'auto', 'gpu' or 'host'");
+    TORCH_CHECK(rowptr_cpu.numel() >= M + 1, "rowptr has fewer than M+1 entries");
     auto w = std::make_shared<TilePlan>();
-    check(ra_tile_plan_create(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
-                              vl.data_ptr<float>(), M, K, N, parse_value_dtype(value_dtype),
-                              &w->plan),
-          what);
+    const int vd = parse_value_dtype(value_dtype);
+    if (build == "host") {
+        auto rp = host_i32(rowptr_cpu);
+        auto ci = host_i32(colind_cpu);
+        auto vl = host_f32(vals_cpu);
+        check(ra_tile_plan_create(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
+                                  vl.data_ptr<float>(), M, K, N, vd, &w->plan),
+              what);
+    } else {
+        const auto dev = rowptr_cpu.is_cuda() ? rowptr_cpu.device()
+                                              : torch::Device(torch::kCUDA, c10::hip::current_device());
+        auto opts = torch::TensorOptions().device(dev);
+        auto rp = rowptr_cpu.to(opts.dtype(torch::kInt32)).contiguous();
+        auto ci = colind_cpu.to(opts.dtype(torch::kInt32)).contiguous();
+        auto vl = vals_cpu.to(opts.dtype(torch::kFloat32)).contiguous();
+        check(ra_tile_plan_create_device(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
+                                         vl.data_ptr<float>(), M, K, N, vd, current_stream(),
+                                         &w->plan),
+              what);
+    }
     check(ra_tile_plan_get_info(w->plan, &w->info), "tile info");
     w->valid = true;
     return w;
@@ -374,7 +392,11 @@ void bind_tile_props(pybind11::class_<TilePlan, std::shared_ptr<TilePlan>>& c) {
         .def_property_readonly("avg_tc_tile_density",
                                [](const TilePlan& w) { return w.info.avg_tile_density; })
         .def_property_readonly("plan_bytes", [](const TilePlan& w) { return w.info.plan_bytes; })
-        .def_property_readonly("build_ms", [](const TilePlan& w) { return w.info.build_ms; });
+        .def_property_readonly("build_ms", [](const TilePlan& w) { return w.info.build_ms; })
+        .def_property_readonly("value_scale_log2", [](const TilePlan& w) { return w.info.value_scale_log2; })
+        .def_property_readonly("max_window_blocks", [](const TilePlan& w) { return w.info.max_window_blocks; })
+        .def_property_readonly("num_blocks", [](const TilePlan& w) { return w.info.num_blocks; })
+        .def_property_readonly("num_split_segs", [](const TilePlan& w) { return w.info.num_split_segs; });
 }
 
 }  // namespace
@@ -477,12 +499,14 @@ PYBIND11_MODULE(_C, m) {
         const std::string make_name = f.make;
         m.def(f.make,
               [kind, make_name](torch::Tensor rp, torch::Tensor ci, torch::Tensor vl, int M, int K,
-                                int N, std::string value_dtype) {
-                  return make_tile_plan(kind, rp, ci, vl, M, K, N, value_dtype, make_name.c_str());
+                                int N, std::string value_dtype, std::string build) {
+                  return make_tile_plan(kind, rp, ci, vl, M, K, N, value_dtype, build,
+                                        make_name.c_str());
               },
-              "Build the tile plan (host build + upload)", pybind11::arg("rowptr_cpu"),
-              pybind11::arg("colind_cpu"), pybind11::arg("vals_cpu"), pybind11::arg("M"),
-              pybind11::arg("K"), pybind11::arg("N"), pybind11::arg("value_dtype") = "fp16");
+              "Build the tile plan (device build by default; build='host' for the host builder)",
+              pybind11::arg("rowptr_cpu"), pybind11::arg("colind_cpu"), pybind11::arg("vals_cpu"),
+              pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"),
+              pybind11::arg("value_dtype") = "fp16", pybind11::arg("build") = "auto");
         if (kind == RA_TILE_SEGMENT_HYBRID) {
             // run_segment_hybrid_plan(plan, colind, vals, B): colind/vals are kept
             // for ABI compatibility, as in tc/ra_segment_hybrid.cu:546-551.
@@ -515,6 +539,17 @@ PYBIND11_MODULE(_C, m) {
                   pybind11::arg("B"));
         }
     }
+    m.def("export_tile_plan",
+          [](std::shared_ptr<TilePlan> w, std::string name) {
+              TORCH_CHECK(w && w->valid, "Invalid tile plan");
+              int64_t n = 0;
+              check(ra_tile_plan_export(w->plan, name.c_str(), nullptr, &n), "export_tile_plan");
+              auto t = torch::empty({n}, torch::TensorOptions().dtype(name == "vals" ? torch::kInt16 : torch::kInt32));
+              check(ra_tile_plan_export(w->plan, name.c_str(), t.data_ptr(), &n), "export_tile_plan");
+              return t;
+          },
+          "Copy a plan array to the host (block_offsets, atox, win_rows, vals, seg_*, split_*)",
+          pybind11::arg("plan"), pybind11::arg("name"));
     m.def("run_tile_plan_route",
           [](std::shared_ptr<TilePlan> w, torch::Tensor B, std::string route) {
               int r = RA_TILE_ROUTE_F16;

@@ -24,7 +24,8 @@ EXPORTED = [
     "ra_spmm_csr_direct", "ra_spmm_csr_baseline", "ra_zo_bins_host", "ra_zo_plan_create",
     "ra_zo_plan_run", "ra_zo_plan_run_stage", "ra_zo_plan_get_info", "ra_zo_plan_destroy", "ra_tile_host_build",
     "ra_tile_host_get_info", "ra_tile_host_export", "ra_tile_host_destroy",
-    "ra_tile_plan_create", "ra_tile_plan_run", "ra_tile_plan_run_lowp",
+    "ra_tile_plan_create", "ra_tile_plan_create_device", "ra_tile_plan_export",
+    "ra_tile_plan_run", "ra_tile_plan_run_lowp",
     "ra_tile_plan_get_info", "ra_tile_plan_destroy", "ra_convert_f32",
 ]
 
@@ -102,6 +103,9 @@ def load():
         "ra_tile_host_export": (ctypes.c_int, [P, ctypes.c_char_p, P, ctypes.POINTER(I64)]),
         "ra_tile_host_destroy": (None, [P]),
         "ra_tile_plan_create": (ctypes.c_int, [I32, P, P, P, I32, I32, I32, I32, ctypes.POINTER(P)]),
+        "ra_tile_plan_create_device": (ctypes.c_int, [I32, P, P, P, I32, I32, I32, I32, P,
+                                                      ctypes.POINTER(P)]),
+        "ra_tile_plan_export": (ctypes.c_int, [P, ctypes.c_char_p, P, ctypes.POINTER(I64)]),
         "ra_tile_plan_run": (ctypes.c_int, [P, P, P, I32, I32, P]),
         "ra_tile_plan_run_lowp": (ctypes.c_int, [P, P, I32, I32, P, I32, P]),
         "ra_tile_plan_get_info": (ctypes.c_int, [P, ctypes.POINTER(TileInfo)]),
