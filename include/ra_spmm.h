@@ -207,6 +207,15 @@ ra_status ra_zo_bins_host(const int32_t* h_rowptr, int32_t M, int32_t K,
                           int32_t* small_rows, int32_t* chunk_rows, int32_t* chunk_starts,
                           int32_t* empty_rows, ra_zo_info* info);
 ra_status ra_zo_plan_create(const int32_t* h_rowptr, int32_t M, int32_t K, ra_zo_plan** out);
+/* Device binning of the same plan from a device rowptr (one scan on the GPU;
+ * replaces the host O(M) loop of the reference's plan build).  Synchronises
+ * `stream`.  Lists are identical to ra_zo_plan_create's. */
+ra_status ra_zo_plan_create_device(const int32_t* d_rowptr, int32_t M, int32_t K, ra_stream_t stream,
+                                   ra_zo_plan** out);
+/* Copy a plan list to the host: "short_rows" (empty, tiny, short, medium rows),
+ * "chunk_rows", "chunk_starts", "chunk_slot", "split_rows", "split_off".
+ * dst may be NULL to query *count. */
+ra_status ra_zo_plan_export(const ra_zo_plan* plan, const char* name, int32_t* dst, int64_t* count);
 ra_status ra_zo_plan_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
                          const float* d_vals, const float* d_B, float* d_C, int32_t N,
                          ra_stream_t stream);

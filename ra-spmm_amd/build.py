@@ -38,6 +38,7 @@ SOURCES = {
     "csr_kernels.hip": [],
     "tile_kernels.hip": [],
     "tile_build_gpu.hip": [],
+    "zo_build_gpu.hip": [],
 }
 LIB_NAME = "libra_spmm_hip.so"
 

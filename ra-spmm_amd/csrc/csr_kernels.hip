@@ -23,6 +23,7 @@
 #include <mutex>
 
 #include "ra_internal.hpp"
+#include "zo_plan.hpp"
 
 namespace {
 
@@ -31,8 +32,11 @@ constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = kWave * kWavesPerBlock;
 
 // ZO bin thresholds (csr/ra_zero_overhead.cu:55-59).
-constexpr int kTiny = 4, kShort = 16, kMedium = 64, kChunk = 256;
-constexpr uint32_t kSoleFlag = 0x80000000u;
+using ra::kTiny;
+using ra::kShort;
+using ra::kMedium;
+using ra::kChunk;
+using ra::kSoleFlag;
 
 // ------------------------------------------------------------------ packets
 template <typename P> __device__ __forceinline__ P pzero();
@@ -261,16 +265,30 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
 }
 
 // Deterministic merge: C[row] = ((slot0 + slot1) + slot2) + ... per element.
+// One thread per (split row, packet); rows are packed np to a workgroup so
+// narrow N does not idle lanes, and slots are loaded 16 at a time so a hub
+// row's chain of ~200 partials costs ~13 memory round trips, not ~200.  The
+// additions stay in ascending slot order.
 template <typename P>
 __global__ __launch_bounds__(kBlock) void zo_merge_kernel(
     const int32_t* __restrict__ split_rows, const int32_t* __restrict__ split_off,
-    const P* __restrict__ partials, P* __restrict__ Cp, int64_t ldp, int np) {
-    const int r = blockIdx.x;
-    const int qq = blockIdx.y * kBlock + threadIdx.x;
-    if (qq >= np) return;
+    const P* __restrict__ partials, P* __restrict__ Cp, int64_t ldp, int np, int nrows) {
+    constexpr int D = 16;
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t r = t / np;
+    if (r >= nrows) return;
+    const int qq = static_cast<int>(t - r * np);
     const int o0 = split_off[r], o1 = split_off[r + 1];
     P acc = partials[(int64_t)o0 * ldp + qq];
-    for (int o = o0 + 1; o < o1; ++o) acc = padd(acc, partials[(int64_t)o * ldp + qq]);
+    int o = o0 + 1;
+    for (; o + D <= o1; o += D) {
+        P x[D];
+#pragma unroll
+        for (int i = 0; i < D; ++i) x[i] = partials[(int64_t)(o + i) * ldp + qq];
+#pragma unroll
+        for (int i = 0; i < D; ++i) acc = padd(acc, x[i]);
+    }
+    for (; o < o1; ++o) acc = padd(acc, partials[(int64_t)o * ldp + qq]);
     Cp[(int64_t)split_rows[r] * ldp + qq] = acc;
 }
 
@@ -487,13 +505,6 @@ ra_status check_spmm_args(const void* rowptr, const void* colind, const void* va
 }  // namespace
 
 // ============================================================ ZO plan object
-struct ra_zo_plan {
-    ra_zo_info info{};
-    int device = 0;
-    ra::DeviceBuffer chunk_rows, chunk_starts, chunk_slot, short_rows, split_rows, split_off;
-    ra::DeviceBuffer partials;  // grown per N, reused across runs
-    int64_t num_short_total = 0; // empty + tiny + short + medium
-};
 
 extern "C" {
 
@@ -709,15 +720,17 @@ ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
         RA_TRY(s);
     }
     if (plan->info.num_split_rows > 0 && stage != 1) {
-        dim3 grid(plan->info.num_split_rows, (np + kBlock - 1) / kBlock);
+        const int64_t threads = (int64_t)plan->info.num_split_rows * np;
+        const unsigned grid = static_cast<unsigned>((threads + kBlock - 1) / kBlock);
         if (vec)
             zo_merge_kernel<float4><<<grid, kBlock, 0, st>>>(
                 plan->split_rows.get<int32_t>(), plan->split_off.get<int32_t>(),
-                plan->partials.get<float4>(), reinterpret_cast<float4*>(d_C), np, np);
+                plan->partials.get<float4>(), reinterpret_cast<float4*>(d_C), np, np,
+                plan->info.num_split_rows);
         else
             zo_merge_kernel<float><<<grid, kBlock, 0, st>>>(
                 plan->split_rows.get<int32_t>(), plan->split_off.get<int32_t>(),
-                plan->partials.get<float>(), d_C, np, np);
+                plan->partials.get<float>(), d_C, np, np, plan->info.num_split_rows);
         RA_LAUNCH_CHECK("zo_merge_kernel");
     }
     return RA_OK;

@@ -257,11 +257,24 @@ struct ZOPlan {
     ~ZOPlan() { ra_zo_plan_destroy(plan); }
 };
 
-std::shared_ptr<ZOPlan> make_zero_overhead_plan(torch::Tensor rowptr_cpu, int M, int K) {
-    auto rp = host_i32(rowptr_cpu);
-    TORCH_CHECK(rp.numel() >= M + 1, "rowptr has fewer than M+1 entries");
+// build: "auto"/"gpu" bin on the device (a host rowptr is uploaded first),
+// "host" runs the host binning loop.  Both give identical lists.
+std::shared_ptr<ZOPlan> make_zero_overhead_plan(torch::Tensor rowptr_cpu, int M, int K,
+                                                const std::string& build) {
+    TORCH_CHECK(build == "auto" || build == "gpu" || build == "host",
+                "build must be 'auto', 'gpu' or 'host'");
+    TORCH_CHECK(rowptr_cpu.numel() >= M + 1, "rowptr has fewer than M+1 entries");
     auto w = std::make_shared<ZOPlan>();
-    check(ra_zo_plan_create(rp.data_ptr<int32_t>(), M, K, &w->plan), "make_zero_overhead_plan");
+    if (build == "host") {
+        auto rp = host_i32(rowptr_cpu);
+        check(ra_zo_plan_create(rp.data_ptr<int32_t>(), M, K, &w->plan), "make_zero_overhead_plan");
+    } else {
+        const auto dev = rowptr_cpu.is_cuda() ? rowptr_cpu.device()
+                                              : torch::Device(torch::kCUDA, c10::hip::current_device());
+        auto rp = rowptr_cpu.to(torch::TensorOptions().device(dev).dtype(torch::kInt32)).contiguous();
+        check(ra_zo_plan_create_device(rp.data_ptr<int32_t>(), M, K, current_stream(), &w->plan),
+              "make_zero_overhead_plan");
+    }
     check(ra_zo_plan_get_info(w->plan, &w->info), "zero_overhead info");
     w->valid = true;
     return w;
@@ -453,8 +466,22 @@ PYBIND11_MODULE(_C, m) {
         .def_property_readonly("num_split_chunks", [](const ZOPlan& w) { return w.info.num_split_chunks; })
         .def_property_readonly("plan_bytes", [](const ZOPlan& w) { return w.info.plan_bytes; });
     m.def("make_zero_overhead_plan", &make_zero_overhead_plan,
-          "Build the ZERO_OVERHEAD_CSR plan (degree-binned dispatch)", pybind11::arg("rowptr_cpu"),
-          pybind11::arg("M"), pybind11::arg("K"));
+          "Build the ZERO_OVERHEAD_CSR plan (degree-binned dispatch; device binning by default)",
+          pybind11::arg("rowptr_cpu"), pybind11::arg("M"), pybind11::arg("K"),
+          pybind11::arg("build") = "auto");
+    m.def("export_zero_overhead_plan",
+          [](std::shared_ptr<ZOPlan> w, std::string name) {
+              TORCH_CHECK(w && w->valid, "Invalid ZeroOverhead plan");
+              int64_t n = 0;
+              check(ra_zo_plan_export(w->plan, name.c_str(), nullptr, &n), "export_zero_overhead_plan");
+              auto t = torch::empty({n}, torch::TensorOptions().dtype(torch::kInt32));
+              check(ra_zo_plan_export(w->plan, name.c_str(), t.data_ptr<int32_t>(), &n),
+                    "export_zero_overhead_plan");
+              return t;
+          },
+          "Copy a plan list to the host (short_rows, chunk_rows, chunk_starts, chunk_slot, "
+          "split_rows, split_off)",
+          pybind11::arg("plan"), pybind11::arg("name"));
     m.def("run_zero_overhead_plan", &run_zero_overhead_plan, "Run ZERO_OVERHEAD_CSR SpMM",
           pybind11::arg("plan"), pybind11::arg("rowptr"), pybind11::arg("colind"),
           pybind11::arg("vals"), pybind11::arg("B"));

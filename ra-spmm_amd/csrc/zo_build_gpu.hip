@@ -1,0 +1,212 @@
+// zo_build_gpu.hip — device binning of the ZERO_OVERHEAD_CSR plan (cold path).
+//
+// Same lists as the host binning (ra_zo_bins_host + ra_zo_plan_create in
+// csr_kernels.hip), produced from a device rowptr in three launches and one
+// scan: classify every row (bin, chunks, split), exclusive-scan the per-row
+// counters, scatter each row to its list positions.  Reference algorithm:
+// make_ra_zero_overhead_plan, csr/ra_zero_overhead.cu:312-387 (a host loop).
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <chrono>
+#include <string>
+
+#include "ra_internal.hpp"
+#include "zo_plan.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// Per-row counters, scanned together: rows per bin (empty, tiny, short,
+// medium), chunks, split rows, split chunks, sole chunks.
+struct ZoCounts {
+    int32_t c[8];
+};
+
+struct ZoCountsSum {
+    __host__ __device__ ZoCounts operator()(const ZoCounts& a, const ZoCounts& b) const {
+        ZoCounts r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.c[i] = a.c[i] + b.c[i];
+        return r;
+    }
+};
+
+enum { kEmpty = 0, kTinyBin = 1, kShortBin = 2, kMediumBin = 3, kChunks = 4, kSplitRows = 5,
+       kSplitChunks = 6, kSoleChunks = 7 };
+
+// counts[i] for rows i < M, counts[M] = 0 so the exclusive scan's last entry
+// is the total.  flags[0]: non-monotone rows, flags[1]: max long-row length.
+__global__ void zo_classify(const int32_t* __restrict__ rowptr, int M, ZoCounts* __restrict__ counts,
+                            unsigned* __restrict__ flags) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i <= M;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        ZoCounts v;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v.c[k] = 0;
+        if (i < M) {
+            const int64_t d = (int64_t)rowptr[i + 1] - rowptr[i];
+            if (d < 0) atomicAdd(&flags[0], 1u);
+            else if (d == 0) v.c[kEmpty] = 1;
+            else if (d <= ra::kTiny) v.c[kTinyBin] = 1;
+            else if (d <= ra::kShort) v.c[kShortBin] = 1;
+            else if (d <= ra::kMedium) v.c[kMediumBin] = 1;
+            else {
+                const int nch = static_cast<int>((d + ra::kChunk - 1) / ra::kChunk);
+                v.c[kChunks] = nch;
+                if (nch == 1) v.c[kSoleChunks] = 1;
+                else {
+                    v.c[kSplitRows] = 1;
+                    v.c[kSplitChunks] = nch;
+                }
+                atomicMax(&flags[1], static_cast<unsigned>(d));
+            }
+        }
+        counts[i] = v;
+    }
+}
+
+__global__ void zo_scatter(const int32_t* __restrict__ rowptr, int M, const ZoCounts* __restrict__ pre,
+                           int4 bin_base, int32_t* __restrict__ short_rows, int32_t* __restrict__ chunk_rows,
+                           int32_t* __restrict__ chunk_starts, int32_t* __restrict__ chunk_slot,
+                           int32_t* __restrict__ split_rows, int32_t* __restrict__ split_off) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < M;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t start = rowptr[i];
+        const int64_t d = (int64_t)rowptr[i + 1] - start;
+        const ZoCounts& o = pre[i];
+        if (d == 0) short_rows[bin_base.x + o.c[kEmpty]] = static_cast<int32_t>(i);
+        else if (d <= ra::kTiny) short_rows[bin_base.y + o.c[kTinyBin]] = static_cast<int32_t>(i);
+        else if (d <= ra::kShort) short_rows[bin_base.z + o.c[kShortBin]] = static_cast<int32_t>(i);
+        else if (d <= ra::kMedium) short_rows[bin_base.w + o.c[kMediumBin]] = static_cast<int32_t>(i);
+        else {
+            const int nch = static_cast<int>((d + ra::kChunk - 1) / ra::kChunk);
+            const bool sole = nch == 1;
+            const int32_t tag = sole ? static_cast<int32_t>(static_cast<uint32_t>(i) | ra::kSoleFlag)
+                                     : static_cast<int32_t>(i);
+            for (int k = 0; k < nch; ++k) {
+                const int c = o.c[kChunks] + k;
+                chunk_rows[c] = tag;
+                chunk_starts[c] = start + k * ra::kChunk;
+                chunk_slot[c] = sole ? -1 : o.c[kSplitChunks] + k;
+            }
+            if (!sole) {
+                split_rows[o.c[kSplitRows]] = static_cast<int32_t>(i);
+                split_off[o.c[kSplitRows] + 1] = o.c[kSplitChunks] + nch;
+            }
+        }
+        if (i == 0) split_off[0] = 0;
+    }
+}
+
+__global__ void zero_flags(unsigned* flags) {
+    if (threadIdx.x < 2) flags[threadIdx.x] = 0u;
+}
+
+unsigned grid_for(int64_t n) {
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, 1 << 16)));
+}
+
+ra_status gpu_bin(ra_zo_plan* p, const int32_t* rowptr, int32_t M, int32_t K, hipStream_t st) {
+    ra_zo_info& z = p->info;
+    z = ra_zo_info{};
+    z.M = M;
+    z.K = K;
+    (void)hipGetDevice(&p->device);
+    if (M == 0) return RA_OK;
+    size_t scan_bytes = 0;
+    ZoCounts* cnull = nullptr;
+    RA_HIP_TRY(hipcub::DeviceScan::ExclusiveScan(nullptr, scan_bytes, cnull, cnull, ZoCountsSum(), ZoCounts{},
+                                                 M + 1, st));
+    const size_t counts_bytes = ((size_t)(M + 1) * sizeof(ZoCounts) + 255) & ~size_t(255);
+    ra::DeviceBuffer tmp;
+    RA_TRY(tmp.allocate(2 * counts_bytes + ((scan_bytes + 255) & ~size_t(255)) + 256));
+    ZoCounts* counts = tmp.get<ZoCounts>();
+    ZoCounts* pre = reinterpret_cast<ZoCounts*>(tmp.get<char>() + counts_bytes);
+    void* scan_tmp = tmp.get<char>() + 2 * counts_bytes;
+    unsigned* flags = reinterpret_cast<unsigned*>(tmp.get<char>() + 2 * counts_bytes +
+                                                  ((scan_bytes + 255) & ~size_t(255)));
+    zero_flags<<<1, 64, 0, st>>>(flags);
+    zo_classify<<<grid_for(M + 1), kThreads, 0, st>>>(rowptr, M, counts, flags);
+    RA_LAUNCH_CHECK("zo_classify");
+    RA_HIP_TRY(hipcub::DeviceScan::ExclusiveScan(scan_tmp, scan_bytes, counts, pre, ZoCountsSum(), ZoCounts{},
+                                                 M + 1, st));
+    ZoCounts tot;
+    unsigned hflags[2];
+    RA_HIP_TRY(hipMemcpyAsync(&tot, pre + M, sizeof(tot), hipMemcpyDeviceToHost, st));
+    RA_HIP_TRY(hipMemcpyAsync(hflags, flags, sizeof(hflags), hipMemcpyDeviceToHost, st));
+    RA_HIP_TRY(hipStreamSynchronize(st));
+    if (hflags[0]) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: rowptr not monotone");
+
+    z.num_empty = tot.c[kEmpty];
+    z.num_tiny = tot.c[kTinyBin];
+    z.num_short = tot.c[kShortBin];
+    z.num_medium = tot.c[kMediumBin];
+    z.num_small = z.num_tiny + z.num_short + z.num_medium;
+    z.num_chunks = tot.c[kChunks];
+    z.num_sole_chunks = tot.c[kSoleChunks];
+    z.num_split_rows = tot.c[kSplitRows];
+    z.num_split_chunks = tot.c[kSplitChunks];
+    z.num_long = z.num_sole_chunks + z.num_split_rows;
+    z.max_long_chunks = static_cast<int32_t>((static_cast<int64_t>(hflags[1]) + ra::kChunk - 1) / ra::kChunk);
+    z.plan_bytes = (int64_t)sizeof(int32_t) *
+                   ((int64_t)z.num_small + z.num_empty + 3LL * z.num_chunks + 2LL * z.num_split_rows + 1);
+    p->num_short_total = (int64_t)z.num_empty + z.num_small;
+
+    const auto i32 = sizeof(int32_t);
+    RA_TRY(p->short_rows.allocate(std::max<int64_t>(p->num_short_total, 1) * i32));
+    RA_TRY(p->chunk_rows.allocate(std::max(z.num_chunks, 1) * i32));
+    RA_TRY(p->chunk_starts.allocate(std::max(z.num_chunks, 1) * i32));
+    RA_TRY(p->chunk_slot.allocate(std::max(z.num_chunks, 1) * i32));
+    RA_TRY(p->split_rows.allocate(std::max(z.num_split_rows, 1) * i32));
+    RA_TRY(p->split_off.allocate((z.num_split_rows + 1) * i32));
+    const int4 base{0, z.num_empty, z.num_empty + z.num_tiny, z.num_empty + z.num_tiny + z.num_short};
+    zo_scatter<<<grid_for(M), kThreads, 0, st>>>(rowptr, M, pre, base, p->short_rows.get<int32_t>(),
+                                                 p->chunk_rows.get<int32_t>(), p->chunk_starts.get<int32_t>(),
+                                                 p->chunk_slot.get<int32_t>(), p->split_rows.get<int32_t>(),
+                                                 p->split_off.get<int32_t>());
+    RA_LAUNCH_CHECK("zo_scatter");
+    RA_HIP_TRY(hipStreamSynchronize(st));
+    return RA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+ra_status ra_zo_plan_create_device(const int32_t* d_rowptr, int32_t M, int32_t K, ra_stream_t stream,
+                                   ra_zo_plan** out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: out is NULL");
+    *out = nullptr;
+    if (M < 0 || (M > 0 && !d_rowptr)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: bad rowptr");
+    auto p = new (std::nothrow) ra_zo_plan();
+    if (!p) return ra::fail(RA_ERR_OUT_OF_MEMORY, "zo: plan allocation");
+    const ra_status s = gpu_bin(p, d_rowptr, M, K, reinterpret_cast<hipStream_t>(stream));
+    if (s != RA_OK) {
+        delete p;
+        return s;
+    }
+    *out = p;
+    return RA_OK;
+}
+
+ra_status ra_zo_plan_export(const ra_zo_plan* p, const char* name, int32_t* dst, int64_t* count) {
+    if (!p || !name || !count) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo export: NULL argument");
+    const std::string n(name);
+    const ra_zo_info& z = p->info;
+    const ra::DeviceBuffer* b = nullptr;
+    int64_t c = 0;
+    if (n == "short_rows") { b = &p->short_rows; c = p->num_short_total; }
+    else if (n == "chunk_rows") { b = &p->chunk_rows; c = z.num_chunks; }
+    else if (n == "chunk_starts") { b = &p->chunk_starts; c = z.num_chunks; }
+    else if (n == "chunk_slot") { b = &p->chunk_slot; c = z.num_chunks; }
+    else if (n == "split_rows") { b = &p->split_rows; c = z.num_split_rows; }
+    else if (n == "split_off") { b = &p->split_off; c = z.M > 0 ? z.num_split_rows + 1 : 0; }
+    else return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo export: unknown array '" + n + "'");
+    *count = c;
+    if (dst && c > 0) RA_HIP_TRY(hipMemcpy(dst, b->get(), c * sizeof(int32_t), hipMemcpyDeviceToHost));
+    return RA_OK;
+}
+
+}  // extern "C"

@@ -166,3 +166,51 @@ def test_c2_full_size_properties(oracle):
     rhs = 2 * C_zo + ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, B2)
     sc = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl.abs(), (2 * B).abs() + B2.abs())
     assert torch.all((lhs - rhs).abs() <= 1e-5 * sc + 1e-30)
+
+
+ZO_INFO = ("M", "K", "num_tiny", "num_short", "num_medium", "num_long", "num_empty", "num_chunks",
+           "num_split_rows", "max_long_chunks", "num_split_chunks", "plan_bytes")
+ZO_LISTS = ("short_rows", "chunk_rows", "chunk_starts", "chunk_slot", "split_rows", "split_off")
+
+
+@pytest.mark.parametrize("case", ["hubs", "all_empty", "all_long", "one_row", "mixed_large"])
+def test_zero_overhead_device_binning_matches_host_and_oracle(oracle, case):
+    """Device binning (one scan on the GPU) == host binning, list for list, and
+    both agree with the oracle's bins (csr/ra_zero_overhead.cu:331-358)."""
+    print(f"[zo-build] {case}", flush=True)
+    if case == "hubs":
+        g = S.random_csr(3000, 4000, 10.0, seed=5, skew=0.9, empty_frac=0.03, max_deg=3000)
+    elif case == "all_empty":
+        g = S.random_csr(77, 10, 0.0, seed=1)
+    elif case == "all_long":
+        g = S.random_csr(40, 5000, 700.0, seed=2)
+    elif case == "one_row":
+        g = S.random_csr(1, 2000, 1000.0, seed=3)
+    else:
+        g = S.random_csr(200000, 50000, 6.0, seed=4, skew=1.0, empty_frac=0.1, max_deg=20000)
+    rp = torch.from_numpy(g.rowptr)
+    host = ra_spmm.make_zero_overhead_plan(rp, g.M, g.K, build="host")
+    dev = ra_spmm.make_zero_overhead_plan(rp.cuda(), g.M, g.K, build="gpu")
+    for f in ZO_INFO:
+        assert getattr(host, f) == getattr(dev, f), f
+    lists = {n: ra_spmm.export_zero_overhead_plan(dev, n).numpy() for n in ZO_LISTS}
+    for n in ZO_LISTS:
+        np.testing.assert_array_equal(ra_spmm.export_zero_overhead_plan(host, n).numpy(), lists[n], err_msg=n)
+    bins = oracle.zo_bins(g.rowptr)
+    empty = np.flatnonzero(np.diff(g.rowptr) == 0)
+    np.testing.assert_array_equal(lists["short_rows"], np.concatenate([empty, bins["small_rows"]]))
+    np.testing.assert_array_equal(lists["chunk_rows"].astype(np.uint32), bins["chunk_rows"].astype(np.uint32))
+    np.testing.assert_array_equal(lists["chunk_starts"], bins["chunk_starts"])
+    # Split chunks own consecutive slots in chunk order.
+    split = lists["chunk_slot"] >= 0
+    np.testing.assert_array_equal(lists["chunk_slot"][split], np.arange(split.sum()))
+
+
+def test_zero_overhead_run_device_plan_equals_host_plan():
+    g = S.random_csr(3000, 4000, 10.0, seed=7, skew=0.9, empty_frac=0.03, max_deg=3000)
+    rp, ci, vl = _dev(g)
+    B = torch.from_numpy(_B(4000, 128, 3)).cuda()
+    host = ra_spmm.make_zero_overhead_plan(rp.cpu(), g.M, g.K, build="host")
+    dev = ra_spmm.make_zero_overhead_plan(rp, g.M, g.K)
+    assert torch.equal(ra_spmm.run_zero_overhead_plan(host, rp, ci, vl, B),
+                       ra_spmm.run_zero_overhead_plan(dev, rp, ci, vl, B))
