@@ -57,9 +57,10 @@ constexpr RouterTable kReference = {
 
 // MI355X calibration (structure of the tree unchanged; measured on gfx950 with
 // bench.py --sweep over the five BASELINE configs):
-//  - tile gate: host build + upload of the tile plans runs at 0.75-1.5e-8 s
-//    per nnz on the MI355X host (C2 16e6 nnz: 0.12-0.23 s; C4 1.24e8 nnz:
-//    0.93-1.2 s), so the estimate is 1e-8 s per nnz with the same 20 s budget;
+//  - tile gate: the device tile build (sorts and scans on the GPU) runs at
+//    0.4-1.1e-9 s per nnz (C2 1.6e7 nnz: 8-17 ms; C4 1.24e8 nnz: 73-89 ms;
+//    the host builder took 0.75-1.5e-8 s per nnz), so the estimate is 1e-9 s
+//    per nnz with the same 20 s budget;
 //  - FP32-route tile picks go to the CSR family: on the ER graph of config 1
 //    CSR_DIRECT takes 9-14 us against 25-42 us for the FP32 tile route;
 //  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR:
@@ -70,7 +71,7 @@ constexpr RouterTable kReference = {
 //  path on configs 2 and 5).
 constexpr RouterTable kMI355X = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
-    25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-8, 20.0, 5.0f, 25000, 9.0f,
+    25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-9, 20.0, 5.0f, 25000, 9.0f,
     1, 0, 1.5f};
 
 bool tile_family(int p) {

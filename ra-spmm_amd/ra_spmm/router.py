@@ -10,8 +10,8 @@ Bit-identity with the C++ router is by construction:
   * every comparison is float32 value vs float32 threshold, evaluated on the
     exactly representable doubles (``_f32``), which is what the C++ float
     comparisons compute;
-  * the tile gate is 2e-8 * d * M evaluated in doubles from the float32 d, in
-    the C++ order.
+  * the tile gate is plan_s_per_nnz * d * M (2e-8 in the reference table)
+    evaluated in doubles from the float32 d, in the C++ order.
 The reference Python mirror compared float64 d and cv against float64
 literals, which can disagree with its C++ twin next to a threshold; routing on
 canonical float32 features removes that gap.
@@ -70,7 +70,7 @@ class RouterTable:
 
 REFERENCE = RouterTable()
 # Calibrated on gfx950 (values and measurements: csrc/router.cpp, kMI355X).
-MI355X = RouterTable(plan_s_per_nnz=1e-8, fp32_route_csr=True, skewed_to_zo=False, zo_min_cv=1.5)
+MI355X = RouterTable(plan_s_per_nnz=1e-9, fp32_route_csr=True, skewed_to_zo=False, zo_min_cv=1.5)
 TABLES = {"reference": REFERENCE, "mi355x": MI355X}
 
 
