@@ -337,6 +337,7 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 3
+    import ra_spmm
     if args.gcn:
         res = bench_gcn(max(5, args.steps // 20), max(2, args.warmup // 10), args.table)
         if args.details:
@@ -368,7 +369,12 @@ def main(argv=None):
                      "kernel_ms": round(res["kernel_ms"], 5), "bytes_alg": res["bytes_alg"]},
         "cpu_baseline": res.get("cpu_port"),
         "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
-                 "first_exec_ms": round(res["cold_first_exec_ms"], 4)},
+                 "first_exec_ms": round(res["cold_first_exec_ms"], 4),
+                 # SpMM calls after which routing + plan build is repaid against
+                 # CSR_DIRECT, which needs no plan.
+                 "crossover_calls_vs_csr_direct": ra_spmm.smallest_strict_crossover(
+                     0.0, res["csr_direct_ms"], res["cold_route_ms"] + res["cold_build_ms"],
+                     res["ms_per_step"])},
         "path": res["path"],
         "baseline_csr_gflops": round(res["baseline_gflops"], 3),
         "csr_direct_gflops": round(res["csr_direct_gflops"], 3),

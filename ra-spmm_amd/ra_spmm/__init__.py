@@ -30,7 +30,7 @@ from .dispatch import (  # noqa: F401
     DEPLOYED_KERNELS, TILE_KERNELS, benchmark_cusparse, benchmark_cusparse_cold,
     build_kernel_plan, gpu_info_next, make_timing_breakdown, measure_exec_ms, measure_one_ms,
     run_oracle_cold, run_oracle_warm, run_planned_kernel, run_router_cold, run_router_plan,
-    run_router_warm,
+    run_router_warm, smallest_strict_crossover,
 )
 from .router import (  # noqa: F401
     MI355X, REFERENCE, RouterTable, features_from_moments, production_features, route_label,

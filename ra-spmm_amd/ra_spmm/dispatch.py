@@ -61,6 +61,17 @@ def run_planned_kernel(kernel_name, plan, rowptr, colind, vals, B):
     raise ValueError(f"Unknown planned kernel: {kernel_name}")
 
 
+def smallest_strict_crossover(setup_a: float, exec_a: float, setup_b: float, exec_b: float):
+    """Smallest integer K >= 1 with setup_b + K*exec_b < setup_a + K*exec_a,
+    None when b never wins (experiments/conversion_aware_routing.py:47-53).
+    Used to state after how many SpMM calls a plan's build cost is repaid."""
+    import math
+    if exec_b >= exec_a:
+        return None
+    threshold = (setup_b - setup_a) / (exec_a - exec_b)
+    return max(1, math.floor(threshold) + 1)
+
+
 def make_timing_breakdown(plan_ms: float, exec_ms: float, nnz: int, N: int) -> dict:
     """bench/benchmark.cpp:29-37: GFLOP/s = 2*nnz*N / (exec_ms * 1e6)."""
     gflops = (2.0 * nnz * N) / (exec_ms * 1e6) if exec_ms > 0 else 0.0
