@@ -114,7 +114,7 @@ template <int CPL, bool BF16, int KIND>
 __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
     const uint16_t* __restrict__ Bh, int ldb, float* __restrict__ C, float* __restrict__ scratch,
-    int M, int N, int num_items, int nslices, int remap, float unscale) {
+    int M, int N, int num_items, int nslices, int remap, float unscale, int vec_store) {
     typedef typename HalfRun<CPL>::T Run;
     const int lane = threadIdx.x & (kWave - 1);
     int64_t item_blk;
@@ -135,21 +135,27 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
 #pragma unroll
     for (int cc = 0; cc < CPL; ++cc) acc[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Indices and A fragment of step b (block b+q of this lane group).
+    // Indices and A fragment of step b (block b+q of this lane group).  Every
+    // vector-memory instruction costs the same address-unit time whatever its
+    // width, so lane pairs (j, j^1) each load half of the block's 8 indices
+    // with one 16-byte load and swap halves through a lane exchange.
+    const int h = j & 1;
     auto load_step = [&](int b, int (&cols)[8], u16x8& a) {
         const int bq = b + q;
+        int4 mine = make_int4(-1, -1, -1, -1);
+        a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         if (bq < b1) {
-            const int4 c0 = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8);
-            const int4 c1 = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8 + 4);
-            cols[0] = c0.x; cols[1] = c0.y; cols[2] = c0.z; cols[3] = c0.w;
-            cols[4] = c1.x; cols[5] = c1.y; cols[6] = c1.z; cols[7] = c1.w;
-            a = a_half ? *reinterpret_cast<const u16x8*>(vals + (int64_t)bq * 64 + (j & 7) * 8)
-                       : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        } else {
-#pragma unroll
-            for (int v = 0; v < 8; ++v) cols[v] = -1;
-            a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            mine = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8 + h * 4);
+            if (a_half) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)bq * 64 + (j & 7) * 8);
         }
+        int4 other;
+        other.x = __shfl_xor(mine.x, 1, kWave);
+        other.y = __shfl_xor(mine.y, 1, kWave);
+        other.z = __shfl_xor(mine.z, 1, kWave);
+        other.w = __shfl_xor(mine.w, 1, kWave);
+        const int4 lo = h ? other : mine, hi = h ? mine : other;
+        cols[0] = lo.x; cols[1] = lo.y; cols[2] = lo.z; cols[3] = lo.w;
+        cols[4] = hi.x; cols[5] = hi.y; cols[6] = hi.z; cols[7] = hi.w;
     };
     int cols_next[8];
     u16x8 a_next;
@@ -186,11 +192,25 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[cc][r] += __shfl_down(acc[cc][r], 32, kWave);
     if (lane >= 32) return;
+    // The lane's CPL columns are contiguous: 16-byte streaming stores when the
+    // rows allow it (C is written once and never read back here).
+    const bool vec = (CPL % 4 == 0) && vec_store && col + CPL <= N;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int m = 4 * (lane >> 4) + r;
         float* dst = item_row<KIND>(it, C, scratch, w, slot, m, M, N);
         if (!dst) continue;
+        if constexpr (CPL % 4 == 0) {
+            if (vec) {
+#pragma unroll
+                for (int cc = 0; cc < CPL; cc += 4) {
+                    const f32x4 v = {acc[cc][r] * unscale, acc[cc + 1][r] * unscale,
+                                     acc[cc + 2][r] * unscale, acc[cc + 3][r] * unscale};
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst + col + cc));
+                }
+                continue;
+            }
+        }
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc)
             if (col + cc < N) dst[col + cc] = acc[cc][r] * unscale;  // exact: power of two
@@ -396,14 +416,15 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
     const int remap = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
 #define RA_MFMA_CASE(c)                                                                            \
     if (cpl == c) {                                                                                \
         if (bf16)                                                                                  \
             tile_mfma_kernel<c, true, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),    \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale, vec_store); \
         else                                                                                       \
             tile_mfma_kernel<c, false, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),   \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale, vec_store); \
     }
     RA_MFMA_CASE(1)
     RA_MFMA_CASE(2)
