@@ -140,6 +140,31 @@ ra_status ra_features_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_
 /* Synchronises `stream` (one 32-byte readback). */
 ra_status ra_features_device(const int32_t* d_rowptr, int32_t M, int32_t K, int32_t N,
                              ra_stream_t stream, ra_features* out);
+/* Diagnostic ("FULL") structural features of a CSR matrix: row-length skew,
+ * 16x16 tile fill statistics, row-signature locality proxies and 16-row window
+ * scores.  Host arrays; O(nnz log nnz); never used by the deployed decision.
+ * Reference: compute_router_features, router/router_features.cpp:113-432;
+ * analyze_matrix_fn, bindings/ra_bindings.cpp:1993-2049. */
+typedef struct ra_diag_features {
+    float avg_nnz_per_row, std_nnz_per_row, degree_cv, max_to_mean_ratio, frac_dense_rows,
+        skew_ratio, long_row_fraction, long_row_nnz_fraction, top_1_row_nnz_fraction,
+        top_5_row_nnz_fraction;
+    float tile_fill_mean, tile_fill_median, tile_fill_p90, tile_fill_max, tile_fill_variance,
+        tile_occupancy, actual_nnz_coverage, avg_nnz_per_tile, row_window_colspan_compactness,
+        local_row_similarity_proxy, reordered_locality_proxy, locality_gain_proxy,
+        locality_selectivity_proxy, road_likeness_proxy, row_split_affinity_proxy,
+        mixedness_proxy;
+    float tc_candidate_ratio, tc_synergy_proxy, estimated_tc_partition_ratio,
+        estimated_cuda_partition_ratio, irregular_window_fraction, tc_granularity_proxy,
+        redundancy_risk_proxy;
+    int32_t tc_candidate_tiles;
+    int32_t N, M, K;
+    int64_t nnz;  /* rowptr[M] */
+} ra_diag_features;
+
+ra_status ra_analyze_matrix(const int32_t* h_rowptr, const int32_t* h_colind, int32_t M, int32_t K,
+                            int32_t N, ra_diag_features* out);
+
 /* Shared finalisation from exact integer moments. */
 ra_status ra_features_from_moments(int32_t M, int32_t K, int32_t N, int64_t nnz,
                                    int64_t sum_deg_sq, int32_t max_deg, int64_t empty_rows,

@@ -34,6 +34,7 @@ HIP_FLAGS = [
 SOURCES = {
     "common.cpp": [],
     "router.cpp": ["-ffp-contract=off"],
+    "diagnostics.cpp": ["-ffp-contract=off"],
     "tile_build.cpp": [],
     "csr_kernels.hip": [],
     "tile_kernels.hip": [],

@@ -209,6 +209,62 @@ pybind11::dict route_to_dict(const ra_features& f, const ra_route& r, float ms) 
     return d;
 }
 
+// analyze_matrix_fn, bindings/ra_bindings.cpp:1993-2049 (host copy of the CSR).
+ra_diag_features diag_of(torch::Tensor rowptr, torch::Tensor colind, int M, int K, int N) {
+    auto rp = host_i32(rowptr);
+    auto ci = host_i32(colind);
+    TORCH_CHECK(rp.numel() >= M + 1, "rowptr has fewer than M+1 entries");
+    ra_diag_features g{};
+    check(ra_analyze_matrix(rp.data_ptr<int32_t>(), ci.numel() ? ci.data_ptr<int32_t>() : nullptr, M, K, N, &g),
+          "analyze_matrix");
+    return g;
+}
+
+void diag_into(pybind11::dict& d, const ra_diag_features& g) {
+    d["avg_nnz_per_row"] = g.avg_nnz_per_row;
+    d["std_nnz_per_row"] = g.std_nnz_per_row;
+    d["degree_cv"] = g.degree_cv;
+    d["max_to_mean_ratio"] = g.max_to_mean_ratio;
+    d["frac_dense_rows"] = g.frac_dense_rows;
+    d["skew_ratio"] = g.skew_ratio;
+    d["long_row_fraction"] = g.long_row_fraction;
+    d["long_row_nnz_fraction"] = g.long_row_nnz_fraction;
+    d["top_1_row_nnz_fraction"] = g.top_1_row_nnz_fraction;
+    d["top_5_row_nnz_fraction"] = g.top_5_row_nnz_fraction;
+    d["tile_fill_mean"] = g.tile_fill_mean;
+    d["tile_fill_median"] = g.tile_fill_median;
+    d["tile_fill_p90"] = g.tile_fill_p90;
+    d["tile_fill_max"] = g.tile_fill_max;
+    d["tile_fill_variance"] = g.tile_fill_variance;
+    d["tile_occupancy"] = g.tile_occupancy;
+    d["actual_nnz_coverage"] = g.actual_nnz_coverage;
+    d["avg_nnz_per_tile"] = g.avg_nnz_per_tile;
+    d["row_window_colspan_compactness"] = g.row_window_colspan_compactness;
+    d["local_row_similarity_proxy"] = g.local_row_similarity_proxy;
+    d["reordered_locality_proxy"] = g.reordered_locality_proxy;
+    d["locality_gain_proxy"] = g.locality_gain_proxy;
+    d["locality_selectivity_proxy"] = g.locality_selectivity_proxy;
+    d["road_likeness_proxy"] = g.road_likeness_proxy;
+    d["row_split_affinity_proxy"] = g.row_split_affinity_proxy;
+    d["mixedness_proxy"] = g.mixedness_proxy;
+    d["tc_candidate_ratio"] = g.tc_candidate_ratio;
+    d["tc_synergy_proxy"] = g.tc_synergy_proxy;
+    d["estimated_tc_partition_ratio"] = g.estimated_tc_partition_ratio;
+    d["estimated_cuda_partition_ratio"] = g.estimated_cuda_partition_ratio;
+    d["irregular_window_fraction"] = g.irregular_window_fraction;
+    d["tc_granularity_proxy"] = g.tc_granularity_proxy;
+    d["redundancy_risk_proxy"] = g.redundancy_risk_proxy;
+    d["tc_candidate_tiles"] = g.tc_candidate_tiles;
+}
+
+pybind11::dict analyze_matrix(torch::Tensor rowptr, torch::Tensor colind, int M, int K, int N) {
+    const ra_diag_features g = diag_of(rowptr, colind, M, K, N);
+    pybind11::dict d;
+    diag_into(d, g);
+    d["nnz"] = g.nnz;
+    return d;
+}
+
 pybind11::dict make_router_plan(torch::Tensor rowptr, torch::Tensor colind, torch::Tensor vals,
                                 int M, int K, int N, std::string portfolio, std::string table) {
     const auto t0 = std::chrono::high_resolution_clock::now();
@@ -220,10 +276,19 @@ pybind11::dict make_router_plan(torch::Tensor rowptr, torch::Tensor colind, torc
     const auto t1 = std::chrono::high_resolution_clock::now();
     pybind11::dict d =
         route_to_dict(f, r, std::chrono::duration<float, std::milli>(t1 - t0).count());
-    d["feature_set"] = "production_4";
     d["feature_backend"] = backend;
     d["router_table"] = table;
-    (void)colind;
+    if (port == RA_PORTFOLIO_FULL) {
+        // FULL plans carry the diagnostic features (router_dispatch.cpp:1123-1125);
+        // the decision above read only M, d, CV and N, which they share.
+        d["feature_set"] = "full";
+        pybind11::dict fv = d["feature_values"];
+        diag_into(fv, diag_of(rowptr, colind, M, K, N));
+        d["planning_time_ms"] =
+            std::chrono::duration<float, std::milli>(std::chrono::high_resolution_clock::now() - t0).count();
+    } else {
+        d["feature_set"] = "production_4";
+    }
     (void)vals;
     return d;
 }
@@ -588,5 +653,8 @@ PYBIND11_MODULE(_C, m) {
           "Run a tile plan on an explicit route", pybind11::arg("plan"), pybind11::arg("B"),
           pybind11::arg("route"));
 
+    m.def("analyze_matrix", &analyze_matrix,
+          "Diagnostic structural features of a CSR matrix (host computation)", pybind11::arg("rowptr"),
+          pybind11::arg("colind"), pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"));
     m.def("abi_version", &ra_abi_version);
 }

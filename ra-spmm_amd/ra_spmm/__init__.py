@@ -18,7 +18,7 @@ except ImportError as exc:  # pragma: no cover - exercised only on broken instal
         f"(or __graft_entry__.build()). Original error: {exc}") from exc
 
 from ._C import (  # noqa: F401
-    CuSparsePlan, RACommunityTCPlan, RASegmentHybridPlan, RATcDirectPlan, RATilePlan,
+    CuSparsePlan, RACommunityTCPlan, analyze_matrix, RASegmentHybridPlan, RATcDirectPlan, RATilePlan,
     RAZeroOverheadPlan, compute_features, export_tile_plan, export_zero_overhead_plan, make_community_tc_plan, make_cusparse_plan,
     make_router_plan, make_segment_hybrid_plan, make_tc_direct_plan, make_zero_overhead_plan,
     route_features, run_community_tc_plan, run_community_tc_plan_tf32, run_cusparse_plan,

@@ -21,6 +21,7 @@ TABLE_REFERENCE, TABLE_MI355X = 0, 1
 EXPORTED = [
     "ra_abi_version", "ra_status_string", "ra_last_error", "ra_path_name", "ra_reject_name",
     "ra_features_host", "ra_features_device", "ra_features_from_moments", "ra_route_dispatch",
+    "ra_analyze_matrix",
     "ra_spmm_csr_direct", "ra_spmm_csr_baseline", "ra_zo_bins_host", "ra_zo_plan_create",
     "ra_zo_plan_create_device", "ra_zo_plan_export", "ra_zo_plan_run", "ra_zo_plan_run_stage", "ra_zo_plan_get_info", "ra_zo_plan_destroy", "ra_tile_host_build",
     "ra_tile_host_get_info", "ra_tile_host_export", "ra_tile_host_destroy",
@@ -37,6 +38,49 @@ class Features(ctypes.Structure):
                 ("avg", ctypes.c_double), ("std_dev", ctypes.c_double),
                 ("avg_nnz_per_row", ctypes.c_float), ("std_nnz_per_row", ctypes.c_float),
                 ("degree_cv", ctypes.c_float), ("max_to_mean_ratio", ctypes.c_float)]
+
+
+DIAG_FLOAT_FIELDS = (
+    "avg_nnz_per_row",
+    "std_nnz_per_row",
+    "degree_cv",
+    "max_to_mean_ratio",
+    "frac_dense_rows",
+    "skew_ratio",
+    "long_row_fraction",
+    "long_row_nnz_fraction",
+    "top_1_row_nnz_fraction",
+    "top_5_row_nnz_fraction",
+    "tile_fill_mean",
+    "tile_fill_median",
+    "tile_fill_p90",
+    "tile_fill_max",
+    "tile_fill_variance",
+    "tile_occupancy",
+    "actual_nnz_coverage",
+    "avg_nnz_per_tile",
+    "row_window_colspan_compactness",
+    "local_row_similarity_proxy",
+    "reordered_locality_proxy",
+    "locality_gain_proxy",
+    "locality_selectivity_proxy",
+    "road_likeness_proxy",
+    "row_split_affinity_proxy",
+    "mixedness_proxy",
+    "tc_candidate_ratio",
+    "tc_synergy_proxy",
+    "estimated_tc_partition_ratio",
+    "estimated_cuda_partition_ratio",
+    "irregular_window_fraction",
+    "tc_granularity_proxy",
+    "redundancy_risk_proxy",
+)
+
+
+class DiagFeatures(ctypes.Structure):
+    _fields_ = ([(k, ctypes.c_float) for k in DIAG_FLOAT_FIELDS] +
+                [("tc_candidate_tiles", ctypes.c_int32), ("N", ctypes.c_int32), ("M", ctypes.c_int32),
+                 ("K", ctypes.c_int32), ("nnz", ctypes.c_int64)])
 
 
 class Route(ctypes.Structure):
@@ -85,6 +129,7 @@ def load():
         "ra_path_name": (ctypes.c_char_p, [I32]),
         "ra_reject_name": (ctypes.c_char_p, [I32]),
         "ra_features_host": (ctypes.c_int, [P, I32, I32, I32, ctypes.POINTER(Features)]),
+        "ra_analyze_matrix": (ctypes.c_int, [P, P, I32, I32, I32, ctypes.POINTER(DiagFeatures)]),
         "ra_features_device": (ctypes.c_int, [P, I32, I32, I32, P, ctypes.POINTER(Features)]),
         "ra_features_from_moments": (ctypes.c_int, [I32, I32, I32, I64, I64, I32, I64,
                                                     ctypes.POINTER(Features)]),
