@@ -58,9 +58,10 @@ constexpr RouterTable kReference = {
 // MI355X calibration (structure of the tree unchanged; measured on gfx950 with
 // bench.py --sweep over the five BASELINE configs):
 //  - tile gate: the device tile build (sorts and scans on the GPU) runs at
-//    0.4-1.1e-9 s per nnz (C2 1.6e7 nnz: 8-17 ms; C4 1.24e8 nnz: 73-89 ms;
-//    the host builder took 0.75-1.5e-8 s per nnz), so the estimate is 1e-9 s
-//    per nnz with the same 20 s budget;
+//    1.1-1.8e-10 s per nnz (C2 1.6e7 nnz: 2.8 ms; C4 1.24e8 nnz: 13.5 ms),
+//    plus ~3e-10 s per nnz to upload a host CSR (the host builder took
+//    0.75-1.5e-8 s per nnz), so the estimate is 1e-9 s per nnz with the same
+//    20 s budget;
 //  - FP32-route tile picks go to the CSR family: on the ER graph of config 1
 //    CSR_DIRECT takes 9-14 us against 25-42 us for the FP32 tile route;
 //  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR:

@@ -52,16 +52,25 @@ __global__ void validate_csr(const int32_t* __restrict__ rowptr, const int32_t* 
     }
 }
 
-// max |v| as the bit pattern of a non-negative float (monotone as unsigned).
+// max |v| as the bit pattern of a non-negative float (monotone as unsigned):
+// wave, then workgroup reduction through LDS, one atomic per workgroup (the
+// launch is capped at kReduceBlocks workgroups).
+constexpr int kReduceBlocks = 1024;
 __global__ void abs_max_bits(const float* __restrict__ vals, int64_t base, int64_t n,
                              unsigned* __restrict__ out) {
+    __shared__ unsigned part[kThreads / 64];
     unsigned m = 0;
     RA_GRID_STRIDE(t, n) {
         const unsigned b = ra::float_bits(vals[base + t]) & 0x7FFFFFFFu;
         if (b <= 0x7F800000u) m = max(m, b);  // ignore NaN payloads
     }
     for (int off = 32; off > 0; off >>= 1) m = max(m, __shfl_xor(m, off, 64));
-    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < kThreads / 64; ++i) m = max(m, part[i]);
+        atomicMax(out, m);
+    }
 }
 
 __global__ void lead_keys(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind, int M,
@@ -121,11 +130,19 @@ __global__ void mark_new(const uint64_t* __restrict__ keys, int64_t n, int32_t* 
     }
 }
 
-__global__ void count_vectors(const uint64_t* __restrict__ keys, const int32_t* __restrict__ newvec,
-                              int64_t n, int32_t* __restrict__ nvec) {
+// Vectors are numbered in (window, column) order, so the last vector id of a
+// window's entries is the number of vectors in windows <= w.  Windows without
+// entries keep 0 and get the running value from a max-scan.
+__global__ void window_last_vid(const uint64_t* __restrict__ keys, const int32_t* __restrict__ vid, int64_t n,
+                                int32_t* __restrict__ last) {
     RA_GRID_STRIDE(i, n) {
-        if (newvec[i]) atomicAdd(&nvec[keys[i] >> 34], 1);
+        const uint64_t w = keys[i] >> 34;
+        if (i == n - 1 || (keys[i + 1] >> 34) != w) last[w] = vid[i];
     }
+}
+
+__global__ void vectors_from_cum(const int32_t* __restrict__ cum, int W, int32_t* __restrict__ nvec) {
+    RA_GRID_STRIDE(w, (int64_t)W) nvec[w] = cum[w] - (w > 0 ? cum[w - 1] : 0);
 }
 
 __global__ void window_counts(const int32_t* __restrict__ nvec, int W, int limit,
@@ -246,6 +263,9 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, scan2, inull, inull, static_cast<int>(W + 1), st));
     scan_bytes = std::max(scan_bytes, scan2);
     RA_HIP_TRY(hipcub::DeviceReduce::Max(nullptr, red_bytes, inull, inull, static_cast<int>(W), st));
+    size_t scan3 = 0;
+    RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, scan3, inull, inull, hipcub::Max(), static_cast<int>(W), st));
+    scan_bytes = std::max(scan_bytes, scan3);
     size_t red2 = 0;
     RA_HIP_TRY(hipcub::DeviceReduce::Sum(nullptr, red2, inull, inull, static_cast<int>(nn), st));
     red_bytes = std::max(red_bytes, red2);
@@ -282,7 +302,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     // Validation and value scale.
     fill_u32<<<1, kThreads, 0, st>>>(flags, 4);
     validate_csr<<<grid_for(std::max<int64_t>(M, n)), kThreads, 0, st>>>(rowptr, colind, M, K, base, n, flags);
-    abs_max_bits<<<grid_for(n), kThreads, 0, st>>>(vals, base, n, flags + 2);
+    abs_max_bits<<<std::min<unsigned>(grid_for(n), kReduceBlocks), kThreads, 0, st>>>(vals, base, n, flags + 2);
     RA_LAUNCH_CHECK("validate_csr");
     unsigned hflags[4];
     RA_TRY(read_back(hflags, flags, 4, st));
@@ -320,8 +340,17 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tb, newvec, vid, static_cast<int>(n), st));
     }
+    // nvec[w] from the last vector id of each window (no atomics): wvec_start
+    // is used as the temporary for the per-window last ids and their max-scan.
     fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(nvec, W + 1, 0);
-    if (n > 0) count_vectors<<<grid_for(n), kThreads, 0, st>>>(keys2, newvec, n, nvec);
+    fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(wvec_start, W + 1, 0);
+    if (n > 0) {
+        window_last_vid<<<grid_for(n), kThreads, 0, st>>>(keys2, vid, n, wvec_start);
+        size_t tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(tmp, tb, wvec_start, nvec, hipcub::Max(), static_cast<int>(W), st));
+        vectors_from_cum<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), wvec_start);
+        RA_HIP_TRY(hipMemcpyAsync(nvec, wvec_start, W * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
+    }
     window_counts<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), limit, blocks, segs,
                                                     split_slots, is_split);
     fill_i32<<<1, kThreads, 0, st>>>(blocks + W, 1, 0);

@@ -186,26 +186,30 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     }
 
     // D[m][n]: lane holds rows 4*(lane>>4)+r, column n = lane & 15.  Rows m and
-    // m+8 are partial sums of the same window row (block-diagonal A).
+    // m+8 are partial sums of the same window row (block-diagonal A): lanes L
+    // and L^32 exchange them, so both halves hold the window's sums and each
+    // half stores two of its four rows (every lane stores).
 #pragma unroll
     for (int cc = 0; cc < CPL; ++cc)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[cc][r] += __shfl_down(acc[cc][r], 32, kWave);
-    if (lane >= 32) return;
+        for (int r = 0; r < 4; ++r) acc[cc][r] += __shfl_xor(acc[cc][r], 32, kWave);
     // The lane's CPL columns are contiguous: 16-byte streaming stores when the
     // rows allow it (C is written once and never read back here).
     const bool vec = (CPL % 4 == 0) && vec_store && col + CPL <= N;
+    const bool upper = lane >= 32;  // rows 2, 3 of the lane's group of four
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = 4 * (lane >> 4) + r;
+    for (int k = 0; k < 2; ++k) {
+        const int m = 4 * ((lane >> 4) & 1) + (upper ? 2 : 0) + k;
+        float out[CPL];
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) out[cc] = (upper ? acc[cc][2 + k] : acc[cc][k]) * unscale;  // exact
         float* dst = item_row<KIND>(it, C, scratch, w, slot, m, M, N);
         if (!dst) continue;
         if constexpr (CPL % 4 == 0) {
             if (vec) {
 #pragma unroll
                 for (int cc = 0; cc < CPL; cc += 4) {
-                    const f32x4 v = {acc[cc][r] * unscale, acc[cc + 1][r] * unscale,
-                                     acc[cc + 2][r] * unscale, acc[cc + 3][r] * unscale};
+                    const f32x4 v = {out[cc], out[cc + 1], out[cc + 2], out[cc + 3]};
                     __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst + col + cc));
                 }
                 continue;
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
         }
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc)
-            if (col + cc < N) dst[col + cc] = acc[cc][r] * unscale;  // exact: power of two
+            if (col + cc < N) dst[col + cc] = out[cc];
     }
 }
 
