@@ -278,15 +278,17 @@ def sweep(configs, Ns, steps, out_path):
     for cfg in configs:
         g = S.CONFIGS[cfg]()
         rp, ci, vl = g.torch("cuda")
+        host = (rp.cpu(), ci.cpu(), vl.cpu())  # plan builders take host CSR, as in the reference
         for N in Ns:
             B = torch.randn(g.K, N, device="cuda")
             base = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
             scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
+            routed = ra_spmm.route_label(ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N, "MAIN", "mi355x"))
             for label in ["CSR_BASELINE"] + ra_spmm.DEPLOYED_KERNELS:
                 if label in ra_spmm.TILE_KERNELS and N < 16:
                     continue
                 t = time.perf_counter()
-                plan = ra_spmm.build_kernel_plan(label, rp.cpu(), ci.cpu(), vl.cpu(), g.M, g.K, N)
+                plan = ra_spmm.build_kernel_plan(label, *host, g.M, g.K, N)
                 torch.cuda.synchronize()
                 build = (time.perf_counter() - t) * 1e3
                 fn = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
@@ -294,13 +296,13 @@ def sweep(configs, Ns, steps, out_path):
                 err = float(((fn() - base).abs() / (scale + 1e-30)).max())
                 row = {"config": cfg, "N": N, "path": label, "ms": wall, "event_ms": ev,
                        "gflops": 2.0 * g.nnz * N / (wall * 1e-3) / 1e9, "build_ms": build,
-                       "max_rel_err_vs_baseline": err}
+                       "max_rel_err_vs_baseline": err, "routed": label == routed}
                 rows.append(row)
                 log(f"[sweep] {cfg} N={N:4d} {label:22s} {wall:9.3f} ms {row['gflops']:9.1f} GF/s "
                     f"build {build:8.1f} ms err {err:.2e}")
                 del plan
             del B
-        del rp, ci, vl
+        del rp, ci, vl, host
         torch.cuda.empty_cache()
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)

@@ -47,13 +47,14 @@ struct RouterTable {
     int   fp32_route_csr;    // FP32-route picks go to the CSR family instead
     int   skewed_to_zo;      // rule 3 sends skewed graphs to ZERO_OVERHEAD_CSR
     float zo_min_cv;         // CSR_DIRECT picks with cv >= this go to ZERO_OVERHEAD_CSR
+    int   n_uniform_csr;     // rule 2, remaining uniform graphs: N <= -> CSR_DIRECT
 };
 
 // Published thresholds (router/router_dispatch.cpp:1004-1094, ra_router_eval.py:37-124).
 constexpr RouterTable kReference = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 2e-8, 20.0, 5.0f, 25000, 9.0f,
-    0, 0, 1e30f};
+    0, 0, 1e30f, 0};
 
 // MI355X calibration (structure of the tree unchanged; measured on gfx950 with
 // bench.py --sweep over the five BASELINE configs):
@@ -66,6 +67,9 @@ constexpr RouterTable kReference = {
 //    CSR_DIRECT takes 9-14 us against 25-42 us for the FP32 tile route;
 //  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR:
 //    one lane group per hub row is 6.6x slower on config 2.
+//  - rule 2's remaining uniform graphs at N <= 64 go to CSR_DIRECT: at 64
+//    columns the MFMA kernel gathers 8 bytes per lane, and on config 3 CSR_DIRECT
+//    takes 0.210 ms against 0.240 ms for TC_DIRECT (0.49 vs 0.37 ms at N=128).
 //  Rules 1-7 otherwise keep the published thresholds: COMMUNITY_TC for
 //  dense/heavy rows (config 4: 16.5 ms, the fastest path), TC_DIRECT for the
 //  uniform family (config 3), ZERO_OVERHEAD_CSR for extreme skew (the fp32
@@ -73,7 +77,7 @@ constexpr RouterTable kReference = {
 constexpr RouterTable kMI355X = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-9, 20.0, 5.0f, 25000, 9.0f,
-    1, 0, 1.5f};
+    1, 0, 1.5f, 64};
 
 bool tile_family(int p) {
     return p == RA_PATH_TC_DIRECT || p == RA_PATH_COMMUNITY_TC || p == RA_PATH_SEGMENT_HYBRID;
@@ -242,6 +246,10 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
             } else {
                 pick_tile(RA_PATH_TC_DIRECT, "tc_direct_community_wideN", true);
             }
+        } else if (N <= T.n_uniform_csr) {
+            choice = RA_PATH_CSR_DIRECT;
+            reason = "csr_direct_uniform_narrowN";
+            risk = 0.05f;
         } else {
             pick_tile(RA_PATH_TC_DIRECT, "tc_direct_uniform", false);
         }

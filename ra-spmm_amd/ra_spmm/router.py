@@ -66,11 +66,13 @@ class RouterTable:
     fp32_route_csr: bool = False
     skewed_to_zo: bool = False
     zo_min_cv: float = 1e30
+    n_uniform_csr: int = 0
 
 
 REFERENCE = RouterTable()
 # Calibrated on gfx950 (values and measurements: csrc/router.cpp, kMI355X).
-MI355X = RouterTable(plan_s_per_nnz=1e-9, fp32_route_csr=True, skewed_to_zo=False, zo_min_cv=1.5)
+MI355X = RouterTable(plan_s_per_nnz=1e-9, fp32_route_csr=True, skewed_to_zo=False, zo_min_cv=1.5,
+                     n_uniform_csr=64)
 TABLES = {"reference": REFERENCE, "mi355x": MI355X}
 
 
@@ -144,6 +146,8 @@ def route_with_rules(avg_nnz, degree_cv, M, N, nnz=None, *, disabled_rules=(), t
             choice, fp32 = ("CSR_DIRECT", False) if N <= T.n_ultralow_csr else pick("TC_DIRECT")
         elif cv >= _f32(T.cv_comm_lo) and d < _f32(T.d_comm):
             choice, fp32 = ("CSR_DIRECT", False) if N <= T.n_comm_csr else pick("TC_DIRECT", True)
+        elif N <= T.n_uniform_csr:
+            choice = "CSR_DIRECT"
         else:
             choice, fp32 = pick("TC_DIRECT")
     elif 3 not in disabled and cv >= _f32(T.cv_skewed):

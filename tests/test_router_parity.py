@@ -48,7 +48,7 @@ def test_python_equals_cpp_on_threshold_grid(table):
     ds = [1.0, 4.49, 4.5, 4.51, 4.99, 5.0, 6.99, 7.0, 8.99, 9.0, 16.0, 24.99, 25.0, 39.99, 40.0, 500.0]
     cvs = [0.0, 0.19, 0.2, 0.21, 0.69, 0.7, 0.71, 1.09, 1.1, 1.45, 1.46, 1.49, 1.5, 1.79, 1.8,
            2.99, 3.0, 4.99, 5.0, 13.4]
-    Ns = [8, 15, 16, 47, 64, 95, 96, 128, 129, 255, 256, 257, 512]
+    Ns = [8, 15, 16, 47, 64, 65, 95, 96, 128, 129, 255, 256, 257, 512]
     n = 0
     for M, d, cv in itertools.product(Ms, ds, cvs):
         nnz, s2 = _moments_for(M, d, cv)
