@@ -34,3 +34,18 @@ def test_sage_and_gin_operators():
     nz = rs > 0
     np.testing.assert_allclose(sage[nz].sum(1), 1.0, rtol=1e-6)
     assert np.all(sage[~nz] == 0)
+
+
+def test_cross_entropy_matches_torch():
+    import torch
+    import torch.nn.functional as F
+    from ra_spmm.gnn import cross_entropy
+    torch.manual_seed(0)
+    logits = torch.randn(1000, 47, requires_grad=True)
+    y = torch.randint(0, 47, (1000,))
+    a = cross_entropy(logits, y)
+    b = F.cross_entropy(logits, y)
+    torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+    ga, = torch.autograd.grad(a, logits)
+    gb, = torch.autograd.grad(b, logits)
+    torch.testing.assert_close(ga, gb, rtol=1e-6, atol=1e-7)
