@@ -246,6 +246,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     const int64_t n = static_cast<int64_t>(ends[1]) - ends[0];
     if (n < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rowptr not monotone");
     if (n > INT32_MAX) return ra::fail(RA_ERR_UNSUPPORTED, "tile: more than 2^31-1 nonzeros");
+    if (n > 0 && (!colind || !vals)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: colind/vals NULL");
     const int64_t W = (M + ra::kTileWindow - 1) / ra::kTileWindow;
     const int64_t slots = W * ra::kTileWindow;
     const int limit = kind == RA_TILE_SEGMENT_HYBRID ? ra::kTileSegBlocks : ra::kTileDirectSplitBlocks;
@@ -467,8 +468,7 @@ ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, cons
     if (value_dtype != RA_DTYPE_F16 && value_dtype != RA_DTYPE_BF16)
         return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: value_dtype must be F16 or BF16");
     if (M < 0 || K < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: negative dimension");
-    if (M > 0 && (!d_rowptr || !d_colind || !d_vals))
-        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: NULL CSR array");
+    if (M > 0 && !d_rowptr) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rowptr is NULL");
     const auto t0 = std::chrono::steady_clock::now();
     auto p = new (std::nothrow) ra_tile_plan();
     if (!p) return ra::fail(RA_ERR_OUT_OF_MEMORY, "tile: plan allocation");
