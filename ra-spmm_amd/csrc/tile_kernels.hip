@@ -98,15 +98,24 @@ __device__ __forceinline__ float* item_row(const Items& it, float* C, float* scr
 // slices of a window run back to back and share its atox/vals in L2.  With
 // remap on, each XCD (workgroups are dealt round-robin over 8) takes one
 // contiguous range of windows, keeping neighbouring windows in one L2.
-__device__ __forceinline__ void tile_block_coords(int nslices, bool remap, int64_t& item_blk,
+// order bit 0: XCD remap; bit 1: slice slowest (all windows of slice 0, then
+// slice 1, ...), which shrinks the gathered working set to one slice of each
+// B row when B is far larger than the L2.
+__device__ __forceinline__ void tile_block_coords(int nslices, int order, int64_t& item_blk,
                                                   int& slice) {
     int64_t bid = blockIdx.x;
-    if (remap) {
+    if (order & 1) {
         const int64_t nb = gridDim.x, q = nb / 8, r = nb % 8, x = bid % 8, k = bid / 8;
         bid = x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
     }
-    item_blk = bid / nslices;
-    slice = static_cast<int>(bid - item_blk * nslices);
+    if (order & 2) {
+        const int64_t per_slice = gridDim.x / nslices;
+        slice = static_cast<int>(bid / per_slice);
+        item_blk = bid - (int64_t)slice * per_slice;
+    } else {
+        item_blk = bid / nslices;
+        slice = static_cast<int>(bid - item_blk * nslices);
+    }
 }
 
 // ------------------------------------------------------------ MFMA route
@@ -119,7 +128,7 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     const int lane = threadIdx.x & (kWave - 1);
     int64_t item_blk;
     int slice;
-    tile_block_coords(nslices, remap != 0, item_blk, slice);
+    tile_block_coords(nslices, remap, item_blk, slice);
     const int item = __builtin_amdgcn_readfirstlane(
         static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
@@ -237,7 +246,7 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
     const int lane = threadIdx.x & (kWave - 1);
     int64_t item_blk;
     int slice;
-    tile_block_coords(nslices, remap != 0, item_blk, slice);
+    tile_block_coords(nslices, remap, item_blk, slice);
     const int item = __builtin_amdgcn_readfirstlane(
         static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
@@ -398,6 +407,18 @@ int tile_max_cpl() {
     return c;
 }
 
+// RA_TILE_SLICE_MAJOR: 1 = always, 0 = never; unset = when the row is split
+// into 4 or more slices (N > 384), where the whole-row working set is 4x the
+// slice's (C4 N=512: 16.9 -> 16.0 ms; at 2 slices the re-read A stream cancels
+// the gain).
+int tile_slice_major(int nslices) {
+    static const int r = [] {
+        const char* e = std::getenv("RA_TILE_SLICE_MAJOR");
+        return e ? (std::atoi(e) != 0 ? 1 : 0) : -1;
+    }();
+    return r >= 0 ? r : (nslices >= 4 ? 1 : 0);
+}
+
 Items plan_items(const ra_tile_plan* p) {
     Items it{};
     it.block_offsets = p->block_offsets.get<int32_t>();
@@ -417,7 +438,7 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
     int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
     cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
-    const int remap = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
+    const int remap = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices) ? 2 : 0);
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
