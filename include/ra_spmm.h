@@ -276,11 +276,14 @@ typedef struct ra_tile_info {
     int64_t nnz;
     int64_t num_vectors;       /* distinct (window, column) pairs          */
     int64_t plan_bytes;
-    float avg_tile_density;    /* nnz / (8 * 8 * num_blocks)               */
+    float avg_tile_density;    /* nnz / (values per block * num_blocks)    */
     int32_t value_dtype;       /* RA_DTYPE_F16 or RA_DTYPE_BF16            */
     double build_ms;           /* host build + upload                      */
     int32_t value_scale_log2;  /* fp16 plans store v * 2^s (s chosen from   */
-    int32_t pad2_;             /* max|v|), outputs are scaled back by 2^-s */
+                               /* max|v|), outputs are scaled back by 2^-s */
+    int32_t rows_per_window;   /* 8: the reference's 8-row windows, blocks of
+                                * 8 vectors; 16 or 32: tall windows, blocks of
+                                * 32 vectors [rows/16][4][16][8] */
 } ra_tile_info;
 
 /* Host-only build of the tile format (testable without a GPU).
@@ -300,13 +303,16 @@ void ra_tile_host_destroy(ra_tile_host* host);
 ra_status ra_tile_plan_create(int32_t kind, const int32_t* h_rowptr, const int32_t* h_colind,
                               const float* h_vals, int32_t M, int32_t K, int32_t N,
                               int32_t value_dtype, ra_tile_plan** out);
-/* Device build of the same format (sorts and scans on the GPU; the cold-path
- * replacement of the reference's host OpenMP build).  CSR arrays are device
- * pointers; synchronises `stream`.  The result is bit-identical to
- * ra_tile_plan_create on the same input. */
+/* Device build (sorts and scans on the GPU; the cold-path replacement of the
+ * reference's host OpenMP build).  CSR arrays are device pointers; synchronises
+ * `stream`.  rows_per_window: 8 gives the reference's format, bit-identical to
+ * ra_tile_plan_create on the same input; 16 or 32 a tall format (more rows
+ * share each gathered B row); 0 picks the height from the matrix (distinct
+ * (row / h, column) counts and the kernel's memory-instruction cost). */
 ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, const int32_t* d_colind,
                                      const float* d_vals, int32_t M, int32_t K, int32_t N,
-                                     int32_t value_dtype, ra_stream_t stream, ra_tile_plan** out);
+                                     int32_t value_dtype, int32_t rows_per_window, ra_stream_t stream,
+                                     ra_tile_plan** out);
 /* Copy a plan array back to the host (same names as ra_tile_host_export). */
 ra_status ra_tile_plan_export(const ra_tile_plan* plan, const char* name, void* dst,
                               int64_t* count);

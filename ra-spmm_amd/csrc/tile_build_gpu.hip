@@ -20,6 +20,7 @@
 #include <climits>
 #include <cmath>
 #include <cstring>
+#include <cstdlib>
 
 #include "half_convert.hpp"
 #include "ra_internal.hpp"
@@ -82,26 +83,36 @@ __global__ void lead_keys(const int32_t* __restrict__ rowptr, const int32_t* __r
     }
 }
 
-__global__ void place_rows(const uint64_t* __restrict__ sorted, int M, int64_t slots,
-                           int32_t* __restrict__ win_rows, int32_t* __restrict__ pos) {
-    RA_GRID_STRIDE(i, slots) {
-        if (i < M) {
-            const int32_t row = static_cast<int32_t>(sorted[i] & 0xFFFFFFFFu);
-            win_rows[i] = row;
-            pos[row] = static_cast<int32_t>(i);
-        } else {
-            win_rows[i] = -1;
-        }
+// Sorted leading-column order: order[i] = row at position i, pos[row] = i.
+__global__ void place_rows(const uint64_t* __restrict__ sorted, int M, int32_t* __restrict__ order,
+                           int32_t* __restrict__ pos) {
+    RA_GRID_STRIDE(i, (int64_t)M) {
+        const int32_t row = static_cast<int32_t>(sorted[i] & 0xFFFFFFFFu);
+        order[i] = row;
+        pos[row] = static_cast<int32_t>(i);
     }
 }
 
-__global__ void identity_rows(int M, int64_t slots, int32_t* __restrict__ win_rows) {
-    RA_GRID_STRIDE(i, slots) win_rows[i] = i < M ? static_cast<int32_t>(i) : -1;
+// win_rows[slot] = row at that position (identity without an order), -1 pad.
+__global__ void fill_win_rows(const int32_t* __restrict__ order, int M, int64_t slots,
+                              int32_t* __restrict__ win_rows) {
+    RA_GRID_STRIDE(i, slots) {
+        win_rows[i] = i < M ? (order ? order[i] : static_cast<int32_t>(i)) : -1;
+    }
 }
 
-// Key of every nonzero; the row of position p is found by binary search.
+// Window geometry: 2^sb rows per window, vb vectors per block.  sb = 3, vb = 8
+// is the reference's 8-row format; sb = 4 or 5 with vb = 32 is the tall format
+// (16 or 32 rows, one MFMA K of vectors per block).
+struct Layout {
+    int sb;
+    int vb;
+};
+
+// Key of every nonzero: (window << (31 + sb)) | (column << sb) | slot; the row
+// of position p is found by binary search.
 __global__ void entry_keys(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
-                           const int32_t* __restrict__ pos, int M, int64_t base, int64_t n,
+                           const int32_t* __restrict__ pos, int M, int64_t base, int64_t n, int sb,
                            uint64_t* __restrict__ keys, int32_t* __restrict__ idx) {
     RA_GRID_STRIDE(t, n) {
         const int64_t p = base + t;
@@ -112,21 +123,48 @@ __global__ void entry_keys(const int32_t* __restrict__ rowptr, const int32_t* __
             else hi = mid - 1;
         }
         const int64_t slot_pos = pos ? pos[lo] : lo;
-        keys[t] = (static_cast<uint64_t>(slot_pos >> 3) << 34) |
-                  (static_cast<uint64_t>(static_cast<uint32_t>(colind[p])) << 3) |
-                  static_cast<uint64_t>(slot_pos & 7);
-        idx[t] = static_cast<int32_t>(t);
+        keys[t] = (static_cast<uint64_t>(slot_pos >> sb) << (31 + sb)) |
+                  (static_cast<uint64_t>(static_cast<uint32_t>(colind[p])) << sb) |
+                  static_cast<uint64_t>(slot_pos & ((1 << sb) - 1));
+        if (idx) idx[t] = static_cast<int32_t>(t);
     }
 }
 
-__global__ void mark_new(const uint64_t* __restrict__ keys, int64_t n, int32_t* __restrict__ newvec,
+__global__ void mark_new(const uint64_t* __restrict__ keys, int64_t n, int sb, int32_t* __restrict__ newvec,
                          int32_t* __restrict__ newkey) {
     RA_GRID_STRIDE(i, n) {
         const uint64_t k = keys[i];
         const bool first = i == 0;
         const uint64_t prev = first ? 0 : keys[i - 1];
-        newvec[i] = (first || (k >> 3) != (prev >> 3)) ? 1 : 0;
+        newvec[i] = (first || (k >> sb) != (prev >> sb)) ? 1 : 0;
         newkey[i] = (first || k != prev) ? 1 : 0;
+    }
+}
+
+// Distinct (row / h, column) pairs for h = 8, 16, 32 from keys sorted at
+// sb = 5: within a (32-row window, column) run the slots ascend, so a new
+// h-window starts where slot >> log2(h) changes.
+__global__ void count_layouts(const uint64_t* __restrict__ keys, int64_t n, unsigned long long* __restrict__ out) {
+    __shared__ unsigned long long part[3][kThreads / 64];
+    unsigned long long c[3] = {0, 0, 0};
+    RA_GRID_STRIDE(i, n) {
+        const uint64_t k = keys[i];
+        const bool first = i == 0 || (keys[i - 1] >> 5) != (k >> 5);
+        const uint64_t prev = i == 0 ? 0 : keys[i - 1];
+        c[0] += first || ((prev & 31) >> 3) != ((k & 31) >> 3);
+        c[1] += first || ((prev & 31) >> 4) != ((k & 31) >> 4);
+        c[2] += first;
+    }
+    for (int t = 0; t < 3; ++t) {
+        unsigned long long v = c[t];
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if ((threadIdx.x & 63) == 0) part[t][threadIdx.x >> 6] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 3) {
+        unsigned long long v = 0;
+        for (int i = 0; i < kThreads / 64; ++i) v += part[threadIdx.x][i];
+        atomicAdd(&out[threadIdx.x], v);
     }
 }
 
@@ -134,10 +172,10 @@ __global__ void mark_new(const uint64_t* __restrict__ keys, int64_t n, int32_t* 
 // window's entries is the number of vectors in windows <= w.  Windows without
 // entries keep 0 and get the running value from a max-scan.
 __global__ void window_last_vid(const uint64_t* __restrict__ keys, const int32_t* __restrict__ vid, int64_t n,
-                                int32_t* __restrict__ last) {
+                                int wshift, int32_t* __restrict__ last) {
     RA_GRID_STRIDE(i, n) {
-        const uint64_t w = keys[i] >> 34;
-        if (i == n - 1 || (keys[i + 1] >> 34) != w) last[w] = vid[i];
+        const uint64_t w = keys[i] >> wshift;
+        if (i == n - 1 || (keys[i + 1] >> wshift) != w) last[w] = vid[i];
     }
 }
 
@@ -145,11 +183,11 @@ __global__ void vectors_from_cum(const int32_t* __restrict__ cum, int W, int32_t
     RA_GRID_STRIDE(w, (int64_t)W) nvec[w] = cum[w] - (w > 0 ? cum[w - 1] : 0);
 }
 
-__global__ void window_counts(const int32_t* __restrict__ nvec, int W, int limit,
+__global__ void window_counts(const int32_t* __restrict__ nvec, int W, int vb, int limit,
                               int32_t* __restrict__ blocks, int32_t* __restrict__ segs,
                               int32_t* __restrict__ split_slots, int32_t* __restrict__ is_split) {
     RA_GRID_STRIDE(w, (int64_t)W) {
-        const int b = (nvec[w] + ra::kTileVec - 1) / ra::kTileVec;
+        const int b = (nvec[w] + vb - 1) / vb;
         blocks[w] = b;
         const bool split = b > limit;
         const int ns = split ? (b + limit - 1) / limit : 1;
@@ -163,23 +201,28 @@ __global__ void scatter_entries(const uint64_t* __restrict__ keys, const int32_t
                                 const int32_t* __restrict__ vid, const int32_t* __restrict__ newkey,
                                 int64_t n, const float* __restrict__ vals, int64_t base,
                                 const int32_t* __restrict__ block_offsets,
-                                const int32_t* __restrict__ win_vec_start, float vscale, int bf16,
+                                const int32_t* __restrict__ win_vec_start, float vscale, int bf16, Layout L,
                                 int32_t* __restrict__ atox, uint16_t* __restrict__ out) {
+    const int rows = 1 << L.sb;
     RA_GRID_STRIDE(i, n) {
         if (!newkey[i]) continue;
         const uint64_t k = keys[i];
-        const int64_t w = static_cast<int64_t>(k >> 34);
-        const int32_t col = static_cast<int32_t>((k >> 3) & 0x7FFFFFFFu);
-        const int slot = static_cast<int>(k & 7u);
+        const int64_t w = static_cast<int64_t>(k >> (31 + L.sb));
+        const int32_t col = static_cast<int32_t>((k >> L.sb) & 0x7FFFFFFFu);
+        const int slot = static_cast<int>(k & static_cast<uint64_t>(rows - 1));
         const int64_t vlocal = (int64_t)(vid[i] - 1) - win_vec_start[w];
-        const int64_t blk = block_offsets[w] + vlocal / ra::kTileVec;
-        const int kk = static_cast<int>(vlocal % ra::kTileVec);
-        atox[blk * ra::kTileVec + kk] = col;
+        const int64_t blk = block_offsets[w] + vlocal / L.vb;
+        const int kk = static_cast<int>(vlocal % L.vb);
+        atox[blk * L.vb + kk] = col;
         // Duplicates of (window, col, slot) follow in CSR order (stable sort).
         float acc = 0.f + vals[base + idx[i]];
         for (int64_t j = i + 1; j < n && keys[j] == k; ++j) acc += vals[base + idx[j]];
-        out[blk * 64 + slot * ra::kTileVec + kk] =
-            bf16 ? ra::bf16_rne_bits(acc) : ra::half_rne_bits(acc * vscale);
+        // 8-row blocks: [slot][vector]; tall blocks: [slot/16][vector/8][slot%16][vector%8],
+        // the 16-byte run one MFMA lane (row slot%16, K group vector/8) loads.
+        const int64_t at = L.vb == 8 ? blk * 64 + slot * 8 + kk
+                                     : blk * ((int64_t)rows * 32) +
+                                           ((((slot >> 4) * 4 + (kk >> 3)) * 16 + (slot & 15)) * 8 + (kk & 7));
+        out[at] = bf16 ? ra::bf16_rne_bits(acc) : ra::half_rne_bits(acc * vscale);
     }
 }
 
@@ -231,13 +274,35 @@ ra_status read_back(T* dst, const T* src, size_t n, hipStream_t st) {
     return RA_OK;
 }
 
+// Window height for rows_per_window = 0, from the distinct (row / h, column)
+// counts v8, v16, v32.  Cost model: vector-memory instructions per 32 vectors
+// (8 B-row gathers and the index load, plus the A loads: one per 16 rows of a
+// tall block, one per 4 blocks of the 8-row format), so 10 per 32 vectors for
+// h = 8 and 16 and 11 for h = 32.  A tall layout is taken only when the model
+// saves at least 15%: measured on MI355X, the 32-row kernel runs C3 (SBM,
+// N=256) in 0.61 ms against 0.69 ms with 8 rows (model: -30%), and graphs whose
+// rows share few columns (C2, C4, C5) run 2-15% slower with 16 or 32 rows.
+// Tall blocks hold h*32 values; a height whose values would pass 2^31 is skipped.
+int choose_rows(unsigned long long v8, unsigned long long v16, unsigned long long v32, int64_t M) {
+    const double c8 = 10.0 * v8, c16 = 10.0 * v16, c32 = 11.0 * v32;
+    auto fits = [&](int h, unsigned long long v) {
+        const double blocks = static_cast<double>(v) / 32.0 + static_cast<double>((M + h - 1) / h);
+        return blocks * h * 32.0 < static_cast<double>(INT32_MAX);
+    };
+    if (c32 <= 0.85 * c8 && c32 <= c16 && fits(32, v32)) return 32;
+    if (c16 <= 0.85 * c8 && fits(16, v16)) return 16;
+    return 8;
+}
+
 ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const int32_t* colind,
-                    const float* vals, int32_t M, int32_t K, int32_t N, int32_t value_dtype, hipStream_t st) {
+                    const float* vals, int32_t M, int32_t K, int32_t N, int32_t value_dtype, int32_t rows_req,
+                    hipStream_t st) {
     p->info = ra_tile_info{};
     p->info.kind = kind;
     p->info.M = M;
     p->info.K = K;
     p->info.value_dtype = value_dtype;
+    p->info.rows_per_window = rows_req > 0 ? rows_req : ra::kTileWindow;
     if (M == 0 || K == 0 || N < 16) return RA_OK;  // inactive, like the host build
     int32_t ends[2];
     RA_TRY(read_back(&ends[0], rowptr, 1, st));
@@ -247,9 +312,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     if (n < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rowptr not monotone");
     if (n > INT32_MAX) return ra::fail(RA_ERR_UNSUPPORTED, "tile: more than 2^31-1 nonzeros");
     if (n > 0 && (!colind || !vals)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: colind/vals NULL");
-    const int64_t W = (M + ra::kTileWindow - 1) / ra::kTileWindow;
-    const int64_t slots = W * ra::kTileWindow;
-    const int limit = kind == RA_TILE_SEGMENT_HYBRID ? ra::kTileSegBlocks : ra::kTileDirectSplitBlocks;
+    const int64_t Wmax = (M + ra::kTileWindow - 1) / ra::kTileWindow;  // most windows of any layout
     const bool bf16 = value_dtype == RA_DTYPE_BF16;
     const int64_t nn = std::max<int64_t>(n, 1);
 
@@ -261,19 +324,20 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
                                                   static_cast<int>(std::max<int64_t>(nn, M)), 0, 64, st));
     RA_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, inull, inull, static_cast<int>(nn), st));
     size_t scan2 = 0;
-    RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, scan2, inull, inull, static_cast<int>(W + 1), st));
+    RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, scan2, inull, inull, static_cast<int>(Wmax + 1), st));
     scan_bytes = std::max(scan_bytes, scan2);
-    RA_HIP_TRY(hipcub::DeviceReduce::Max(nullptr, red_bytes, inull, inull, static_cast<int>(W), st));
+    RA_HIP_TRY(hipcub::DeviceReduce::Max(nullptr, red_bytes, inull, inull, static_cast<int>(Wmax), st));
     size_t scan3 = 0;
-    RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, scan3, inull, inull, hipcub::Max(), static_cast<int>(W), st));
+    RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, scan3, inull, inull, hipcub::Max(),
+                                                 static_cast<int>(Wmax), st));
     scan_bytes = std::max(scan_bytes, scan3);
     size_t red2 = 0;
     RA_HIP_TRY(hipcub::DeviceReduce::Sum(nullptr, red2, inull, inull, static_cast<int>(nn), st));
     red_bytes = std::max(red_bytes, red2);
     const size_t tmp_bytes = std::max({sort_bytes, scan_bytes, red_bytes});
 
-    const size_t need = 256 * 24 + tmp_bytes + nn * (2 * 8 + 2 * 4 + 3 * 4) +
-                        std::max<int64_t>(M, 1) * (2 * 8 + 4) + (W + 1) * 4 * 9 + 64;
+    const size_t need = 256 * 26 + tmp_bytes + nn * (2 * 8 + 2 * 4 + 3 * 4) +
+                        std::max<int64_t>(M, 1) * (2 * 8 + 4 + 4) + (Wmax + 1) * 4 * 9 + 64;
     Scratch s;
     RA_TRY(s.buf.allocate(need));
     size_t off = 0;
@@ -288,17 +352,19 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     uint64_t* rkeys = s.take<uint64_t>(std::max<int64_t>(M, 1), off);
     uint64_t* rkeys2 = s.take<uint64_t>(std::max<int64_t>(M, 1), off);
     int32_t* pos = s.take<int32_t>(std::max<int64_t>(M, 1), off);
-    int32_t* nvec = s.take<int32_t>(W + 1, off);
-    int32_t* wvec_start = s.take<int32_t>(W + 1, off);
-    int32_t* blocks = s.take<int32_t>(W + 1, off);
-    int32_t* segs = s.take<int32_t>(W + 1, off);
-    int32_t* seg_start = s.take<int32_t>(W + 1, off);
-    int32_t* split_slots = s.take<int32_t>(W + 1, off);
-    int32_t* slot_start = s.take<int32_t>(W + 1, off);
-    int32_t* is_split = s.take<int32_t>(W + 1, off);
-    int32_t* split_idx = s.take<int32_t>(W + 1, off);
+    int32_t* order = s.take<int32_t>(std::max<int64_t>(M, 1), off);
+    int32_t* nvec = s.take<int32_t>(Wmax + 1, off);
+    int32_t* wvec_start = s.take<int32_t>(Wmax + 1, off);
+    int32_t* blocks = s.take<int32_t>(Wmax + 1, off);
+    int32_t* segs = s.take<int32_t>(Wmax + 1, off);
+    int32_t* seg_start = s.take<int32_t>(Wmax + 1, off);
+    int32_t* split_slots = s.take<int32_t>(Wmax + 1, off);
+    int32_t* slot_start = s.take<int32_t>(Wmax + 1, off);
+    int32_t* is_split = s.take<int32_t>(Wmax + 1, off);
+    int32_t* split_idx = s.take<int32_t>(Wmax + 1, off);
     unsigned* flags = s.take<unsigned>(4, off);
     int32_t* red_out = s.take<int32_t>(2, off);
+    unsigned long long* layout_counts = s.take<unsigned long long>(3, off);
 
     // Validation and value scale.
     fill_u32<<<1, kThreads, 0, st>>>(flags, 4);
@@ -314,30 +380,68 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     p->info.value_scale_log2 = bf16 ? 0 : ra::f16_value_scale_log2(vmax);
     const float vscale = std::ldexp(1.0f, p->info.value_scale_log2);
 
-    // Row -> window slot.
-    RA_TRY(p->win_rows.allocate(slots * sizeof(int32_t)));
+    // Row order: COMMUNITY_TC sorts rows by leading column (ties by row).
     const int32_t* pos_ptr = nullptr;
+    const int32_t* order_ptr = nullptr;
     if (kind == RA_TILE_COMMUNITY_TC) {
         lead_keys<<<grid_for(M), kThreads, 0, st>>>(rowptr, colind, M, rkeys);
         // Keys are unique, so the radix sort yields the stable leading-column order.
         size_t tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, rkeys, rkeys2, M, 0, 63, st));
-        place_rows<<<grid_for(slots), kThreads, 0, st>>>(rkeys2, M, slots, p->win_rows.get<int32_t>(), pos);
+        place_rows<<<grid_for(M), kThreads, 0, st>>>(rkeys2, M, order, pos);
         pos_ptr = pos;
-    } else {
-        identity_rows<<<grid_for(slots), kThreads, 0, st>>>(M, slots, p->win_rows.get<int32_t>());
+        order_ptr = order;
     }
+    RA_LAUNCH_CHECK("row order");
+
+    // Window height: asked for, or the cheapest by the address-unit model from
+    // the distinct (row / h, column) counts of one sort at h = 32.
+    int rows = rows_req;
+    if (rows == 0) {
+        // RA_TILE_ROWS=8|16|32 fixes the automatic choice (measurement runs).
+        if (const char* e = std::getenv("RA_TILE_ROWS")) rows = std::atoi(e);
+    }
+    if (rows == 0) {
+        rows = ra::kTileWindow;
+        if (n > 0) {
+            fill_u32<<<1, kThreads, 0, st>>>(reinterpret_cast<unsigned*>(layout_counts), 6);
+            entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, 5, keys, nullptr);
+            int wb = 0;
+            while ((int64_t(1) << wb) < (M + 31) / 32) ++wb;
+            size_t tb = tmp_bytes;
+            RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, keys, keys2, static_cast<int>(n), 0, 36 + wb, st));
+            count_layouts<<<std::min<unsigned>(grid_for(n), kReduceBlocks), kThreads, 0, st>>>(keys2, n,
+                                                                                                layout_counts);
+            RA_LAUNCH_CHECK("count_layouts");
+            unsigned long long v[3];
+            RA_TRY(read_back(v, layout_counts, 3, st));
+            rows = choose_rows(v[0], v[1], v[2], M);
+        }
+    }
+    if (rows != 8 && rows != 16 && rows != 32)
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rows per window must be 8, 16 or 32");
+    const Layout L{rows == 8 ? 3 : rows == 16 ? 4 : 5, rows == 8 ? 8 : 32};
+    const int64_t W = (M + rows - 1) / rows;
+    const int64_t slots = W * rows;
+    // Split limits in vectors: 64 8-vector blocks for SEGMENT_HYBRID (the
+    // reference rule), kTileDirectSplitBlocks of them for the other kinds.
+    const int limit =
+        (kind == RA_TILE_SEGMENT_HYBRID ? ra::kTileSegBlocks : ra::kTileDirectSplitBlocks) * ra::kTileVec / L.vb;
+    p->info.rows_per_window = rows;
+    RA_TRY(p->win_rows.allocate(slots * sizeof(int32_t)));
+    fill_win_rows<<<grid_for(slots), kThreads, 0, st>>>(order_ptr, M, slots, p->win_rows.get<int32_t>());
     RA_LAUNCH_CHECK("window slots");
 
     // Sort nonzeros by (window, column, slot), stable in CSR position.
     int wbits = 0;
     while ((int64_t(1) << wbits) < W) ++wbits;
+    const int wshift = 31 + L.sb;
     if (n > 0) {
-        entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, keys, idx);
+        entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, L.sb, keys, idx);
         size_t tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, keys2, idx, idx2, static_cast<int>(n),
-                                                      0, 34 + wbits, st));
-        mark_new<<<grid_for(n), kThreads, 0, st>>>(keys2, n, newvec, newkey);
+                                                      0, wshift + wbits, st));
+        mark_new<<<grid_for(n), kThreads, 0, st>>>(keys2, n, L.sb, newvec, newkey);
         tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tb, newvec, vid, static_cast<int>(n), st));
     }
@@ -346,13 +450,13 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(nvec, W + 1, 0);
     fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(wvec_start, W + 1, 0);
     if (n > 0) {
-        window_last_vid<<<grid_for(n), kThreads, 0, st>>>(keys2, vid, n, wvec_start);
+        window_last_vid<<<grid_for(n), kThreads, 0, st>>>(keys2, vid, n, wshift, wvec_start);
         size_t tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(tmp, tb, wvec_start, nvec, hipcub::Max(), static_cast<int>(W), st));
         vectors_from_cum<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), wvec_start);
         RA_HIP_TRY(hipMemcpyAsync(nvec, wvec_start, W * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
     }
-    window_counts<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), limit, blocks, segs,
+    window_counts<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), L.vb, limit, blocks, segs,
                                                     split_slots, is_split);
     fill_i32<<<1, kThreads, 0, st>>>(blocks + W, 1, 0);
     fill_i32<<<1, kThreads, 0, st>>>(segs + W, 1, 0);
@@ -391,16 +495,17 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     int32_t reds[2];
     RA_TRY(read_back(reds, red_out, 2, st));
     const int64_t nblocks = totals[0];
-    if (nblocks > INT32_MAX / 64) return ra::fail(RA_ERR_UNSUPPORTED, "tile: too many blocks for int32 offsets");
+    const int64_t block_vals = (int64_t)rows * L.vb;  // values per block
+    if (nblocks * block_vals > INT32_MAX) return ra::fail(RA_ERR_UNSUPPORTED, "tile: too many blocks for int32 offsets");
 
     // atox, values.
-    RA_TRY(p->atox.allocate(std::max<int64_t>(nblocks, 1) * ra::kTileVec * sizeof(int32_t)));
-    RA_TRY(p->vals.allocate(std::max<int64_t>(nblocks, 1) * 64 * sizeof(uint16_t)));
-    fill_i32<<<grid_for(nblocks * ra::kTileVec), kThreads, 0, st>>>(p->atox.get<int32_t>(), nblocks * ra::kTileVec, -1);
-    fill_u16<<<grid_for(nblocks * 64), kThreads, 0, st>>>(p->vals.get<uint16_t>(), nblocks * 64);
+    RA_TRY(p->atox.allocate(std::max<int64_t>(nblocks, 1) * L.vb * sizeof(int32_t)));
+    RA_TRY(p->vals.allocate(std::max<int64_t>(nblocks, 1) * block_vals * sizeof(uint16_t)));
+    fill_i32<<<grid_for(nblocks * L.vb), kThreads, 0, st>>>(p->atox.get<int32_t>(), nblocks * L.vb, -1);
+    fill_u16<<<grid_for(nblocks * block_vals), kThreads, 0, st>>>(p->vals.get<uint16_t>(), nblocks * block_vals);
     if (n > 0)
         scatter_entries<<<grid_for(n), kThreads, 0, st>>>(keys2, idx2, vid, newkey, n, vals, base, boff,
-                                                          wvec_start, vscale, bf16 ? 1 : 0,
+                                                          wvec_start, vscale, bf16 ? 1 : 0, L,
                                                           p->atox.get<int32_t>(), p->vals.get<uint16_t>());
     RA_LAUNCH_CHECK("scatter_entries");
 
@@ -429,10 +534,10 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     I.max_window_blocks = reds[0];
     I.nnz = reds[1];
     I.num_vectors = totals[1];
-    I.avg_tile_density = nblocks > 0 ? static_cast<float>(static_cast<double>(I.nnz) / (64.0 * nblocks)) : 0.f;
-    I.plan_bytes = static_cast<int64_t>(4 * (slots + (W + 1) + nblocks * ra::kTileVec + 4 * nseg + nsplit +
-                                             nsplit + 1) +
-                                        2 * nblocks * 64);
+    I.avg_tile_density =
+        nblocks > 0 ? static_cast<float>(static_cast<double>(I.nnz) / (static_cast<double>(block_vals) * nblocks)) : 0.f;
+    I.plan_bytes = static_cast<int64_t>(4 * (slots + (W + 1) + nblocks * L.vb + 4 * nseg + nsplit + nsplit + 1) +
+                                        2 * nblocks * block_vals);
     p->num_items = static_cast<int32_t>(nseg);
     return RA_OK;
 }
@@ -442,9 +547,11 @@ const ra::DeviceBuffer* plan_array(const ra_tile_plan* p, const std::string& n, 
     const int64_t W = I.num_windows;
     elem = 4;
     if (n == "block_offsets") { count = I.active ? W + 1 : 0; return &p->block_offsets; }
-    if (n == "atox") { count = (int64_t)I.num_blocks * ra::kTileVec; return &p->atox; }
-    if (n == "win_rows") { count = W * ra::kTileWindow; return &p->win_rows; }
-    if (n == "vals") { elem = 2; count = (int64_t)I.num_blocks * 64; return &p->vals; }
+    const int64_t rows = I.rows_per_window > 0 ? I.rows_per_window : ra::kTileWindow;
+    const int64_t vb = rows == ra::kTileWindow ? ra::kTileVec : 32;
+    if (n == "atox") { count = (int64_t)I.num_blocks * vb; return &p->atox; }
+    if (n == "win_rows") { count = W * rows; return &p->win_rows; }
+    if (n == "vals") { elem = 2; count = (int64_t)I.num_blocks * rows * vb; return &p->vals; }
     if (n == "seg_window") { count = I.num_segments; return &p->seg_window; }
     if (n == "seg_bbegin") { count = I.num_segments; return &p->seg_bbegin; }
     if (n == "seg_bend") { count = I.num_segments; return &p->seg_bend; }
@@ -460,7 +567,8 @@ extern "C" {
 
 ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, const int32_t* d_colind,
                                      const float* d_vals, int32_t M, int32_t K, int32_t N,
-                                     int32_t value_dtype, ra_stream_t stream, ra_tile_plan** out) {
+                                     int32_t value_dtype, int32_t rows_per_window, ra_stream_t stream,
+                                     ra_tile_plan** out) {
     if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: out is NULL");
     *out = nullptr;
     if (kind < RA_TILE_TC_DIRECT || kind > RA_TILE_SEGMENT_HYBRID)
@@ -472,7 +580,11 @@ ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, cons
     const auto t0 = std::chrono::steady_clock::now();
     auto p = new (std::nothrow) ra_tile_plan();
     if (!p) return ra::fail(RA_ERR_OUT_OF_MEMORY, "tile: plan allocation");
-    const ra_status s = gpu_build(p, kind, d_rowptr, d_colind, d_vals, M, K, N, value_dtype,
+    if (rows_per_window != 0 && rows_per_window != 8 && rows_per_window != 16 && rows_per_window != 32) {
+        delete p;
+        return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rows_per_window must be 0 (auto), 8, 16 or 32");
+    }
+    const ra_status s = gpu_build(p, kind, d_rowptr, d_colind, d_vals, M, K, N, value_dtype, rows_per_window,
                                   reinterpret_cast<hipStream_t>(stream));
     if (s != RA_OK) {
         delete p;

@@ -82,14 +82,14 @@ __device__ __forceinline__ void item_range(const Items& it, int i, int& w, int& 
     slot = it.seg_slot[i];
 }
 
-// Destination of window slot m (0..7): a C row, or a partial-slot row.
-template <int KIND>
+// Destination of window slot m (0..H-1): a C row, or a partial-slot row.
+template <int KIND, int H = ra::kTileWindow>
 __device__ __forceinline__ float* item_row(const Items& it, float* C, float* scratch, int w,
                                            int slot, int m, int M, int N) {
-    if (slot >= 0) return scratch + ((int64_t)slot * ra::kTileWindow + m) * N;
+    if (slot >= 0) return scratch + ((int64_t)slot * H + m) * N;
     int row;
-    if constexpr (KIND == RA_TILE_COMMUNITY_TC) row = it.win_rows[w * ra::kTileWindow + m];
-    else row = w * ra::kTileWindow + m;
+    if constexpr (KIND == RA_TILE_COMMUNITY_TC) row = it.win_rows[(int64_t)w * H + m];
+    else row = w * H + m;
     if (row < 0 || row >= M) return nullptr;
     return C + (int64_t)row * N;
 }
@@ -230,11 +230,172 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     }
 }
 
-// ------------------------------------------------------------ FP32 route
 __device__ __forceinline__ float stored_to_f32(uint16_t h, bool bf16) {
     if (bf16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
+
+// ------------------------------------------------- MFMA route, tall windows
+// Windows of H = 16*RG rows; a block is 32 vectors (one MFMA K) with values
+// [RG][4][16][8]: lane (j, q) of row group g loads the 16-byte run of row
+// 16g + j over vectors 8q..8q+7.  Every gathered B row feeds RG MFMAs (one per
+// row group), so a B row shared by several of the H rows is gathered once.
+// Per step: one index load (lane pairs exchange halves), 8 B-row gathers,
+// RG A loads; no block-diagonal padding.
+template <int CPL, bool BF16, int KIND, int RG>
+__global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
+    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
+    const uint16_t* __restrict__ Bh, int ldb, float* __restrict__ C, float* __restrict__ scratch,
+    int M, int N, int num_items, int nslices, int order, float unscale, int vec_store) {
+    typedef typename HalfRun<CPL>::T Run;
+    constexpr int H = 16 * RG;
+    constexpr int BV = H * 32;  // values per block
+    const int lane = threadIdx.x & (kWave - 1);
+    int64_t item_blk;
+    int slice;
+    tile_block_coords(nslices, order, item_blk, slice);
+    const int item = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
+    if (item >= num_items) return;
+    int w, b0, b1, slot;
+    item_range(it, item, w, b0, b1, slot);
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int h = j & 1;
+    const int col = slice * (16 * CPL) + j * CPL;
+    const bool col_ok = col < ldb;
+
+    f32x4 acc[RG][CPL];
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) acc[g][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto load_step = [&](int b, int (&cols)[8], u16x8 (&a)[RG]) {
+        const int4 mine = *reinterpret_cast<const int4*>(atox + (int64_t)b * 32 + q * 8 + h * 4);
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+            a[g] = *reinterpret_cast<const u16x8*>(vals + (int64_t)b * BV + ((g * 4 + q) * 16 + j) * 8);
+        int4 other;
+        other.x = __shfl_xor(mine.x, 1, kWave);
+        other.y = __shfl_xor(mine.y, 1, kWave);
+        other.z = __shfl_xor(mine.z, 1, kWave);
+        other.w = __shfl_xor(mine.w, 1, kWave);
+        const int4 lo = h ? other : mine, hi = h ? mine : other;
+        cols[0] = lo.x; cols[1] = lo.y; cols[2] = lo.z; cols[3] = lo.w;
+        cols[4] = hi.x; cols[5] = hi.y; cols[6] = hi.z; cols[7] = hi.w;
+    };
+    int cols_next[8];
+    u16x8 a_next[RG];
+    if (b0 < b1) load_step(b0, cols_next, a_next);
+    for (int b = b0; b < b1; ++b) {
+        int cols[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) cols[v] = cols_next[v];
+        u16x8 a[RG];
+#pragma unroll
+        for (int g = 0; g < RG; ++g) a[g] = a_next[g];
+        Run raw[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            if (cols[v] >= 0 && col_ok)
+                raw[v] = *reinterpret_cast<const Run*>(Bh + (int64_t)cols[v] * ldb + col);
+            else
+                raw[v] = Run{};
+        }
+        if (b + 1 < b1) load_step(b + 1, cols_next, a_next);
+#pragma unroll
+        for (int cc = 0; cc < CPL; ++cc) {
+            u16x8 bop;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) bop[v] = run_elem<CPL>(raw[v], cc);
+#pragma unroll
+            for (int g = 0; g < RG; ++g) acc[g][cc] = mfma32<BF16>(a[g], bop, acc[g][cc]);
+        }
+    }
+
+    // D of row group g: lane holds rows 16g + 4q + r, column j's CPL outputs.
+    const bool vec = (CPL % 4 == 0) && vec_store && col + CPL <= N;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * g + 4 * q + r;
+            float* dst = item_row<KIND, H>(it, C, scratch, w, slot, m, M, N);
+            if (!dst) continue;
+            float out[CPL];
+#pragma unroll
+            for (int cc = 0; cc < CPL; ++cc) out[cc] = acc[g][cc][r] * unscale;  // exact: power of two
+            if constexpr (CPL % 4 == 0) {
+                if (vec) {
+#pragma unroll
+                    for (int cc = 0; cc < CPL; cc += 4) {
+                        const f32x4 v = {out[cc], out[cc + 1], out[cc + 2], out[cc + 3]};
+                        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst + col + cc));
+                    }
+                    continue;
+                }
+            }
+#pragma unroll
+            for (int cc = 0; cc < CPL; ++cc)
+                if (col + cc < N) dst[col + cc] = out[cc];
+        }
+    }
+}
+
+// FP32 route on tall windows: one wave per (item, 64-column slice), lane = one
+// column, H accumulators; vectors in ascending column order, exact fp32 FMA of
+// the stored value (as the 8-row FP32 kernel).
+template <int KIND, int RG>
+__global__ __launch_bounds__(kBlock) void tile_fp32_tall_kernel(
+    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
+    float unscale, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch,
+    int M, int N, int num_items, int nslices, int order) {
+    constexpr int H = 16 * RG;
+    constexpr int BV = H * 32;
+    const int lane = threadIdx.x & (kWave - 1);
+    int64_t item_blk;
+    int slice;
+    tile_block_coords(nslices, order, item_blk, slice);
+    const int item = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
+    if (item >= num_items) return;
+    int w, b0, b1, slot;
+    item_range(it, item, w, b0, b1, slot);
+    const int col = slice * 64 + lane;
+    float acc[H];
+#pragma unroll
+    for (int m = 0; m < H; ++m) acc[m] = 0.f;
+    const bool bf = bf16vals != 0;
+    for (int b = b0; b < b1; ++b) {
+        for (int v0 = 0; v0 < 32; v0 += 8) {
+            int c[8];
+            float bv[8];
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                c[v] = atox[(int64_t)b * 32 + v0 + v];
+                bv[v] = (c[v] >= 0 && col < N) ? B[(int64_t)c[v] * N + col] : 0.f;
+            }
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                if (c[v] < 0) break;  // padding sits at the end of the last block
+                const int kk = v0 + v;
+#pragma unroll
+                for (int m = 0; m < H; ++m) {
+                    const uint16_t s = vals[(int64_t)b * BV + (((m >> 4) * 4 + (kk >> 3)) * 16 + (m & 15)) * 8 + (kk & 7)];
+                    acc[m] = __builtin_fmaf(stored_to_f32(s, bf) * unscale, bv[v], acc[m]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < H; ++m) {
+        float* dst = item_row<KIND, H>(it, C, scratch, w, slot, m, M, N);
+        if (dst && col < N) dst[col] = acc[m];
+    }
+}
+
+// ------------------------------------------------------------ FP32 route
 
 // One wavefront per (item, slice of 64*F columns); lane covers F consecutive
 // columns.  VEC: F-wide vector loads/stores (needs N % F == 0 and alignment).
@@ -313,18 +474,18 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
 __global__ __launch_bounds__(kBlock) void tile_merge_kernel(
     const int32_t* __restrict__ split_windows, const int32_t* __restrict__ split_offsets,
     const int32_t* __restrict__ win_rows, const float* __restrict__ scratch, float* __restrict__ C,
-    int M, int N) {
+    int M, int N, int H) {
     const int sw = blockIdx.x;
     const int64_t e = (int64_t)blockIdx.y * kBlock + threadIdx.x;
-    if (e >= (int64_t)ra::kTileWindow * N) return;
+    if (e >= (int64_t)H * N) return;
     const int m = static_cast<int>(e / N);
     const int n = static_cast<int>(e - (int64_t)m * N);
-    const int64_t slot_row = (int64_t)split_windows[sw] * ra::kTileWindow + m;
+    const int64_t slot_row = (int64_t)split_windows[sw] * H + m;
     const int row = win_rows ? win_rows[slot_row] : static_cast<int>(slot_row);
     if (row < 0 || row >= M) return;
     const int o0 = split_offsets[sw], o1 = split_offsets[sw + 1];
-    float acc = scratch[((int64_t)o0 * ra::kTileWindow + m) * N + n];
-    for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * ra::kTileWindow + m) * N + n];
+    float acc = scratch[((int64_t)o0 * H + m) * N + n];
+    for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * H + m) * N + n];
     C[(int64_t)row * N + n] = acc;
 }
 
@@ -493,34 +654,92 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
 
 ra_status launch_merge(const ra_tile_plan* p, float* C, int N, hipStream_t st) {
     if (p->info.num_split_windows == 0) return RA_OK;
-    dim3 grid(p->info.num_split_windows, (8 * N + kBlock - 1) / kBlock);
+    const int H = p->info.rows_per_window;
+    dim3 grid(p->info.num_split_windows, static_cast<unsigned>(((int64_t)H * N + kBlock - 1) / kBlock));
     const int32_t* wr = p->info.kind == RA_TILE_COMMUNITY_TC ? p->win_rows.get<int32_t>() : nullptr;
     tile_merge_kernel<<<grid, kBlock, 0, st>>>(p->split_windows.get<int32_t>(),
                                                p->split_offsets.get<int32_t>(), wr,
-                                               p->scratch.get<float>(), C, p->info.M, N);
+                                               p->scratch.get<float>(), C, p->info.M, N, H);
     RA_LAUNCH_CHECK("tile_merge_kernel");
     return RA_OK;
+}
+
+template <int KIND, int RG>
+ra_status launch_mfma_tall(const ra_tile_plan* p, const uint16_t* Bh, int ldb, bool bf16, float* C,
+                           float* scratch, int N, hipStream_t st) {
+    const int M = p->info.M;
+    const Items it = plan_items(p);
+    int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
+    cpl = std::min(cpl, tile_max_cpl());
+    const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
+    const int order = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices) ? 2 : 0);
+    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
+    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
+#define RA_TALL_CASE(c)                                                                                  \
+    if (cpl == c) {                                                                                      \
+        if (bf16)                                                                                        \
+            tile_mfma_tall_kernel<c, true, KIND, RG><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(), \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, order, unscale, vec_store); \
+        else                                                                                             \
+            tile_mfma_tall_kernel<c, false, KIND, RG><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(), \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, order, unscale, vec_store); \
+    }
+    RA_TALL_CASE(1)
+    RA_TALL_CASE(2)
+    RA_TALL_CASE(4)
+    RA_TALL_CASE(8)
+#undef RA_TALL_CASE
+    RA_LAUNCH_CHECK("tile_mfma_tall_kernel");
+    return RA_OK;
+}
+
+template <int KIND, int RG>
+ra_status launch_fp32_tall(const ra_tile_plan* p, const float* B, float* C, float* scratch, int N,
+                           hipStream_t st) {
+    const Items it = plan_items(p);
+    const int nslices = (N + 63) / 64;
+    const int order = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
+    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    tile_fp32_tall_kernel<KIND, RG><<<grid, kBlock, 0, st>>>(
+        it, p->atox.get<int32_t>(), p->vals.get<uint16_t>(), p->info.value_dtype == RA_DTYPE_BF16 ? 1 : 0,
+        std::ldexp(1.0f, -p->info.value_scale_log2), B, C, scratch, p->info.M, N, p->num_items, nslices, order);
+    RA_LAUNCH_CHECK("tile_fp32_tall_kernel");
+    return RA_OK;
+}
+
+template <int KIND>
+ra_status launch_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* B32, bool bf16,
+                      bool fp32_route, float* C, float* scratch, int N, hipStream_t st) {
+    switch (p->info.rows_per_window) {
+        case 16:
+            return fp32_route ? launch_fp32_tall<KIND, 1>(p, B32, C, scratch, N, st)
+                              : launch_mfma_tall<KIND, 1>(p, Bh, ldb, bf16, C, scratch, N, st);
+        case 32:
+            return fp32_route ? launch_fp32_tall<KIND, 2>(p, B32, C, scratch, N, st)
+                              : launch_mfma_tall<KIND, 2>(p, Bh, ldb, bf16, C, scratch, N, st);
+        default:
+            return fp32_route ? launch_fp32_kind<KIND>(p, B32, C, scratch, N, st)
+                              : launch_mfma_kind<KIND>(p, Bh, ldb, bf16, C, scratch, N, st);
+    }
 }
 
 ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* B32, bool bf16,
                      bool fp32_route, float* C, int N, hipStream_t st) {
     float* scratch = nullptr;
     if (p->info.num_split_segs > 0) {
-        RA_TRY(p->scratch.ensure((size_t)p->info.num_split_segs * ra::kTileWindow * N * sizeof(float)));
+        RA_TRY(p->scratch.ensure((size_t)p->info.num_split_segs * p->info.rows_per_window * N * sizeof(float)));
         scratch = p->scratch.get<float>();
     }
     switch (p->info.kind) {
         case RA_TILE_TC_DIRECT:
-            RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_TC_DIRECT>(p, B32, C, scratch, N, st)
-                              : launch_mfma_kind<RA_TILE_TC_DIRECT>(p, Bh, ldb, bf16, C, scratch, N, st));
+            RA_TRY(launch_kind<RA_TILE_TC_DIRECT>(p, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
             break;
         case RA_TILE_COMMUNITY_TC:
-            RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_COMMUNITY_TC>(p, B32, C, scratch, N, st)
-                              : launch_mfma_kind<RA_TILE_COMMUNITY_TC>(p, Bh, ldb, bf16, C, scratch, N, st));
+            RA_TRY(launch_kind<RA_TILE_COMMUNITY_TC>(p, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
             break;
         default:
-            RA_TRY(fp32_route ? launch_fp32_kind<RA_TILE_SEGMENT_HYBRID>(p, B32, C, scratch, N, st)
-                              : launch_mfma_kind<RA_TILE_SEGMENT_HYBRID>(p, Bh, ldb, bf16, C, scratch, N, st));
+            RA_TRY(launch_kind<RA_TILE_SEGMENT_HYBRID>(p, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
             break;
     }
     RA_TRY(launch_merge(p, C, N, st));

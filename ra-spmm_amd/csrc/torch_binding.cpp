@@ -399,7 +399,9 @@ int parse_value_dtype(const std::string& s) {
 std::shared_ptr<TilePlan> make_tile_plan(int kind, torch::Tensor rowptr_cpu, torch::Tensor colind_cpu,
                                          torch::Tensor vals_cpu, int M, int K, int N,
                                          const std::string& value_dtype, const std::string& build,
-                                         const char* what) {
+                                         int rows_per_window, const char* what) {
+    TORCH_CHECK(build != "host" || rows_per_window == 0 || rows_per_window == 8,
+                "the host builder makes 8-row windows only");
     TORCH_CHECK(build == "auto" || build == "gpu" || build == "host",
                 "build must be 'auto', 'gpu' or 'host'");
     TORCH_CHECK(rowptr_cpu.numel() >= M + 1, "rowptr has fewer than M+1 entries");
@@ -420,8 +422,8 @@ std::shared_ptr<TilePlan> make_tile_plan(int kind, torch::Tensor rowptr_cpu, tor
         auto ci = colind_cpu.to(opts.dtype(torch::kInt32)).contiguous();
         auto vl = vals_cpu.to(opts.dtype(torch::kFloat32)).contiguous();
         check(ra_tile_plan_create_device(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
-                                         vl.data_ptr<float>(), M, K, N, vd, current_stream(),
-                                         &w->plan),
+                                         vl.data_ptr<float>(), M, K, N, vd, rows_per_window,
+                                         current_stream(), &w->plan),
               what);
     }
     check(ra_tile_plan_get_info(w->plan, &w->info), "tile info");
@@ -474,7 +476,8 @@ void bind_tile_props(pybind11::class_<TilePlan, std::shared_ptr<TilePlan>>& c) {
         .def_property_readonly("value_scale_log2", [](const TilePlan& w) { return w.info.value_scale_log2; })
         .def_property_readonly("max_window_blocks", [](const TilePlan& w) { return w.info.max_window_blocks; })
         .def_property_readonly("num_blocks", [](const TilePlan& w) { return w.info.num_blocks; })
-        .def_property_readonly("num_split_segs", [](const TilePlan& w) { return w.info.num_split_segs; });
+        .def_property_readonly("num_split_segs", [](const TilePlan& w) { return w.info.num_split_segs; })
+        .def_property_readonly("rows_per_window", [](const TilePlan& w) { return w.info.rows_per_window; });
 }
 
 }  // namespace
@@ -591,14 +594,16 @@ PYBIND11_MODULE(_C, m) {
         const std::string make_name = f.make;
         m.def(f.make,
               [kind, make_name](torch::Tensor rp, torch::Tensor ci, torch::Tensor vl, int M, int K,
-                                int N, std::string value_dtype, std::string build) {
-                  return make_tile_plan(kind, rp, ci, vl, M, K, N, value_dtype, build,
+                                int N, std::string value_dtype, std::string build, int rows_per_window) {
+                  return make_tile_plan(kind, rp, ci, vl, M, K, N, value_dtype, build, rows_per_window,
                                         make_name.c_str());
               },
-              "Build the tile plan (device build by default; build='host' for the host builder)",
+              "Build the tile plan (device build by default; build='host' for the host builder; "
+              "rows_per_window 0 = chosen from the matrix, 8 = the reference's windows, 16/32 = tall)",
               pybind11::arg("rowptr_cpu"), pybind11::arg("colind_cpu"), pybind11::arg("vals_cpu"),
               pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"),
-              pybind11::arg("value_dtype") = "fp16", pybind11::arg("build") = "auto");
+              pybind11::arg("value_dtype") = "fp16", pybind11::arg("build") = "auto",
+              pybind11::arg("rows_per_window") = 0);
         if (kind == RA_TILE_SEGMENT_HYBRID) {
             // run_segment_hybrid_plan(plan, colind, vals, B): colind/vals are kept
             // for ABI compatibility, as in tc/ra_segment_hybrid.cu:546-551.

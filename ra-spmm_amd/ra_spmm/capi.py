@@ -105,7 +105,7 @@ class TileInfo(ctypes.Structure):
         "num_split_windows", "num_split_segs", "max_window_blocks")] + [
         ("nnz", ctypes.c_int64), ("num_vectors", ctypes.c_int64), ("plan_bytes", ctypes.c_int64),
         ("avg_tile_density", ctypes.c_float), ("value_dtype", ctypes.c_int32),
-        ("build_ms", ctypes.c_double), ("value_scale_log2", ctypes.c_int32), ("pad2_", ctypes.c_int32)]
+        ("build_ms", ctypes.c_double), ("value_scale_log2", ctypes.c_int32), ("rows_per_window", ctypes.c_int32)]
 
 
 _lib = None
@@ -150,7 +150,7 @@ def load():
         "ra_tile_host_export": (ctypes.c_int, [P, ctypes.c_char_p, P, ctypes.POINTER(I64)]),
         "ra_tile_host_destroy": (None, [P]),
         "ra_tile_plan_create": (ctypes.c_int, [I32, P, P, P, I32, I32, I32, I32, ctypes.POINTER(P)]),
-        "ra_tile_plan_create_device": (ctypes.c_int, [I32, P, P, P, I32, I32, I32, I32, P,
+        "ra_tile_plan_create_device": (ctypes.c_int, [I32, P, P, P, I32, I32, I32, I32, I32, P,
                                                       ctypes.POINTER(P)]),
         "ra_tile_plan_export": (ctypes.c_int, [P, ctypes.c_char_p, P, ctypes.POINTER(I64)]),
         "ra_tile_plan_run": (ctypes.c_int, [P, P, P, I32, I32, P]),

@@ -49,7 +49,7 @@ GRAPHS = {
 def _compare(g, kind, value_dtype, N=64):
     rp, ci, vl = (torch.from_numpy(np.ascontiguousarray(a)) for a in (g.rowptr, g.colind, g.vals))
     host = MAKE[kind](rp, ci, vl, g.M, g.K, N, value_dtype, build="host")
-    dev = MAKE[kind](rp.cuda(), ci.cuda(), vl.cuda(), g.M, g.K, N, value_dtype, build="gpu")
+    dev = MAKE[kind](rp.cuda(), ci.cuda(), vl.cuda(), g.M, g.K, N, value_dtype, build="gpu", rows_per_window=8)
     for f in INFO:
         assert getattr(host, f) == getattr(dev, f), f
     for a in ARRAYS:
@@ -81,7 +81,7 @@ def test_device_build_runs_identically():
 def test_device_build_inactive_and_invalid():
     g = GRAPHS["skewed"]()
     rp, ci, vl = g.torch("cuda")
-    p = ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, 8, build="gpu")
+    p = ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, 8, build="gpu", rows_per_window=8)
     assert p.valid and not p.active
     bad = ci.clone()
     bad[5] = g.K
