@@ -284,6 +284,10 @@ typedef struct ra_tile_info {
     int32_t rows_per_window;   /* 8: the reference's 8-row windows, blocks of
                                 * 8 vectors; 16 or 32: tall windows, blocks of
                                 * 32 vectors [rows/16][4][16][8] */
+    int32_t col_parts;         /* 1, or P column ranges: windows are cut into
+                                * P cells (partition-major) run one partition
+                                * at a time, accumulating into C in order */
+    int32_t pad3_;
 } ra_tile_info;
 
 /* Host-only build of the tile format (testable without a GPU).

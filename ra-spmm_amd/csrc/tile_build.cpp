@@ -270,6 +270,7 @@ ra_status ra_tile_host_get_info(const ra_tile_host* h, ra_tile_info* info) {
     info->value_dtype = h->value_dtype;
     info->value_scale_log2 = h->value_scale_log2;
     info->rows_per_window = ra::kTileWindow;
+    info->col_parts = 1;
     info->build_ms = h->build_ms;
     return RA_OK;
 }

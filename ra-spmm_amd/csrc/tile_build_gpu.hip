@@ -111,9 +111,11 @@ struct Layout {
 
 // Key of every nonzero: (window << (31 + sb)) | (column << sb) | slot; the row
 // of position p is found by binary search.
+// With column partitions the "window" of a key is the cell
+// part * W + window, part = column / cols_per_part (partition-major cells).
 __global__ void entry_keys(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
                            const int32_t* __restrict__ pos, int M, int64_t base, int64_t n, int sb,
-                           uint64_t* __restrict__ keys, int32_t* __restrict__ idx) {
+                           int cols_per_part, int64_t W, uint64_t* __restrict__ keys, int32_t* __restrict__ idx) {
     RA_GRID_STRIDE(t, n) {
         const int64_t p = base + t;
         int lo = 0, hi = M - 1;  // last row with rowptr[row] <= p
@@ -123,7 +125,8 @@ __global__ void entry_keys(const int32_t* __restrict__ rowptr, const int32_t* __
             else hi = mid - 1;
         }
         const int64_t slot_pos = pos ? pos[lo] : lo;
-        keys[t] = (static_cast<uint64_t>(slot_pos >> sb) << (31 + sb)) |
+        const int64_t cell = (int64_t)(colind[p] / cols_per_part) * W + (slot_pos >> sb);
+        keys[t] = (static_cast<uint64_t>(cell) << (31 + sb)) |
                   (static_cast<uint64_t>(static_cast<uint32_t>(colind[p])) << sb) |
                   static_cast<uint64_t>(slot_pos & ((1 << sb) - 1));
         if (idx) idx[t] = static_cast<int32_t>(t);
@@ -303,6 +306,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     p->info.K = K;
     p->info.value_dtype = value_dtype;
     p->info.rows_per_window = rows_req > 0 ? rows_req : ra::kTileWindow;
+    p->info.col_parts = 1;
     if (M == 0 || K == 0 || N < 16) return RA_OK;  // inactive, like the host build
     int32_t ends[2];
     RA_TRY(read_back(&ends[0], rowptr, 1, st));
@@ -312,7 +316,19 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     if (n < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rowptr not monotone");
     if (n > INT32_MAX) return ra::fail(RA_ERR_UNSUPPORTED, "tile: more than 2^31-1 nonzeros");
     if (n > 0 && (!colind || !vals)) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: colind/vals NULL");
-    const int64_t Wmax = (M + ra::kTileWindow - 1) / ra::kTileWindow;  // most windows of any layout
+    // Column partitions: P > 1 cuts every window into P cells by column range
+    // (partition-major), so that the kernels can run one partition at a time
+    // and keep the gathered working set (K / P rows of B) near the L2 size.
+    // Auto: P = 8 for long rows (nnz / M >= 128) over wide B (K >= 65536),
+    // where the per-partition accumulation into C costs little against the
+    // gathers; RA_TILE_COL_PARTS fixes it (1, 2, 4, 8 or 16).
+    int P = (K >= 65536 && n >= 128LL * M) ? 8 : 1;
+    if (const char* e = std::getenv("RA_TILE_COL_PARTS")) {
+        const int v = std::atoi(e);
+        if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16) P = v;
+    }
+    const int cols_per_part = static_cast<int>((static_cast<int64_t>(K) + P - 1) / P);
+    const int64_t Wmax = (M + ra::kTileWindow - 1) / ra::kTileWindow * P;  // most cells of any layout
     const bool bf16 = value_dtype == RA_DTYPE_BF16;
     const int64_t nn = std::max<int64_t>(n, 1);
 
@@ -405,7 +421,8 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         rows = ra::kTileWindow;
         if (n > 0) {
             fill_u32<<<1, kThreads, 0, st>>>(reinterpret_cast<unsigned*>(layout_counts), 6);
-            entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, 5, keys, nullptr);
+            entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, 5, INT32_MAX,
+                                                         (M + 31) / 32, keys, nullptr);
             int wb = 0;
             while ((int64_t(1) << wb) < (M + 31) / 32) ++wb;
             size_t tb = tmp_bytes;
@@ -432,12 +449,14 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     fill_win_rows<<<grid_for(slots), kThreads, 0, st>>>(order_ptr, M, slots, p->win_rows.get<int32_t>());
     RA_LAUNCH_CHECK("window slots");
 
-    // Sort nonzeros by (window, column, slot), stable in CSR position.
+    // Sort nonzeros by (cell, column, slot), stable in CSR position.
+    const int64_t NC = W * P;
     int wbits = 0;
-    while ((int64_t(1) << wbits) < W) ++wbits;
+    while ((int64_t(1) << wbits) < NC) ++wbits;
     const int wshift = 31 + L.sb;
     if (n > 0) {
-        entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, L.sb, keys, idx);
+        entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, L.sb, cols_per_part, W,
+                                                     keys, idx);
         size_t tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, keys2, idx, idx2, static_cast<int>(n),
                                                       0, wshift + wbits, st));
@@ -447,27 +466,27 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     }
     // nvec[w] from the last vector id of each window (no atomics): wvec_start
     // is used as the temporary for the per-window last ids and their max-scan.
-    fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(nvec, W + 1, 0);
-    fill_i32<<<grid_for(W + 1), kThreads, 0, st>>>(wvec_start, W + 1, 0);
+    fill_i32<<<grid_for(NC + 1), kThreads, 0, st>>>(nvec, NC + 1, 0);
+    fill_i32<<<grid_for(NC + 1), kThreads, 0, st>>>(wvec_start, NC + 1, 0);
     if (n > 0) {
         window_last_vid<<<grid_for(n), kThreads, 0, st>>>(keys2, vid, n, wshift, wvec_start);
         size_t tb = tmp_bytes;
-        RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(tmp, tb, wvec_start, nvec, hipcub::Max(), static_cast<int>(W), st));
-        vectors_from_cum<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), wvec_start);
-        RA_HIP_TRY(hipMemcpyAsync(nvec, wvec_start, W * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
+        RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(tmp, tb, wvec_start, nvec, hipcub::Max(), static_cast<int>(NC), st));
+        vectors_from_cum<<<grid_for(NC), kThreads, 0, st>>>(nvec, static_cast<int>(NC), wvec_start);
+        RA_HIP_TRY(hipMemcpyAsync(nvec, wvec_start, NC * sizeof(int32_t), hipMemcpyDeviceToDevice, st));
     }
-    window_counts<<<grid_for(W), kThreads, 0, st>>>(nvec, static_cast<int>(W), L.vb, limit, blocks, segs,
+    window_counts<<<grid_for(NC), kThreads, 0, st>>>(nvec, static_cast<int>(NC), L.vb, limit, blocks, segs,
                                                     split_slots, is_split);
-    fill_i32<<<1, kThreads, 0, st>>>(blocks + W, 1, 0);
-    fill_i32<<<1, kThreads, 0, st>>>(segs + W, 1, 0);
-    fill_i32<<<1, kThreads, 0, st>>>(split_slots + W, 1, 0);
-    fill_i32<<<1, kThreads, 0, st>>>(is_split + W, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(blocks + NC, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(segs + NC, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(split_slots + NC, 1, 0);
+    fill_i32<<<1, kThreads, 0, st>>>(is_split + NC, 1, 0);
     RA_LAUNCH_CHECK("window counts");
-    RA_TRY(p->block_offsets.allocate((W + 1) * sizeof(int32_t)));
+    RA_TRY(p->block_offsets.allocate((NC + 1) * sizeof(int32_t)));
     int32_t* boff = p->block_offsets.get<int32_t>();
     {
         size_t tb = tmp_bytes;
-        const int wn = static_cast<int>(W + 1);
+        const int wn = static_cast<int>(NC + 1);
         RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, nvec, wvec_start, wn, st));
         tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, blocks, boff, wn, st));
@@ -478,7 +497,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, is_split, split_idx, wn, st));
         tb = tmp_bytes;
-        RA_HIP_TRY(hipcub::DeviceReduce::Max(tmp, tb, blocks, red_out, static_cast<int>(W), st));
+        RA_HIP_TRY(hipcub::DeviceReduce::Max(tmp, tb, blocks, red_out, static_cast<int>(NC), st));
         if (n > 0) {
             tb = tmp_bytes;
             RA_HIP_TRY(hipcub::DeviceReduce::Sum(tmp, tb, newkey, red_out + 1, static_cast<int>(n), st));
@@ -487,11 +506,11 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         }
     }
     int32_t totals[6];  // blocks, vectors, segments, slots, split windows
-    RA_TRY(read_back(&totals[0], boff + W, 1, st));
-    RA_TRY(read_back(&totals[1], wvec_start + W, 1, st));
-    RA_TRY(read_back(&totals[2], seg_start + W, 1, st));
-    RA_TRY(read_back(&totals[3], slot_start + W, 1, st));
-    RA_TRY(read_back(&totals[4], split_idx + W, 1, st));
+    RA_TRY(read_back(&totals[0], boff + NC, 1, st));
+    RA_TRY(read_back(&totals[1], wvec_start + NC, 1, st));
+    RA_TRY(read_back(&totals[2], seg_start + NC, 1, st));
+    RA_TRY(read_back(&totals[3], slot_start + NC, 1, st));
+    RA_TRY(read_back(&totals[4], split_idx + NC, 1, st));
     int32_t reds[2];
     RA_TRY(read_back(reds, red_out, 2, st));
     const int64_t nblocks = totals[0];
@@ -517,15 +536,25 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     RA_TRY(p->seg_slot.allocate(nseg * sizeof(int32_t)));
     RA_TRY(p->split_windows.allocate(std::max<int64_t>(nsplit, 1) * sizeof(int32_t)));
     RA_TRY(p->split_offsets.allocate((nsplit + 1) * sizeof(int32_t)));
-    fill_segments<<<grid_for(W), kThreads, 0, st>>>(boff, seg_start, slot_start, split_idx, static_cast<int>(W),
+    fill_segments<<<grid_for(NC), kThreads, 0, st>>>(boff, seg_start, slot_start, split_idx, static_cast<int>(NC),
                                                     limit, p->seg_window.get<int32_t>(), p->seg_bbegin.get<int32_t>(),
                                                     p->seg_bend.get<int32_t>(), p->seg_slot.get<int32_t>(),
                                                     p->split_windows.get<int32_t>(), p->split_offsets.get<int32_t>());
     RA_LAUNCH_CHECK("fill_segments");
     RA_HIP_TRY(hipStreamSynchronize(st));
 
+    // First segment and first split window of every partition (cells are
+    // partition-major, so each partition's items are one contiguous run).
+    p->part_items.assign(P + 1, 0);
+    p->part_splits.assign(P + 1, 0);
+    for (int q = 1; q <= P; ++q) {
+        RA_TRY(read_back(&p->part_items[q], seg_start + (int64_t)q * W, 1, st));
+        RA_TRY(read_back(&p->part_splits[q], split_idx + (int64_t)q * W, 1, st));
+    }
+
     ra_tile_info& I = p->info;
     I.active = 1;
+    I.col_parts = P;
     I.num_windows = static_cast<int32_t>(W);
     I.num_blocks = static_cast<int32_t>(nblocks);
     I.num_segments = static_cast<int32_t>(nseg);
@@ -536,7 +565,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     I.num_vectors = totals[1];
     I.avg_tile_density =
         nblocks > 0 ? static_cast<float>(static_cast<double>(I.nnz) / (static_cast<double>(block_vals) * nblocks)) : 0.f;
-    I.plan_bytes = static_cast<int64_t>(4 * (slots + (W + 1) + nblocks * L.vb + 4 * nseg + nsplit + nsplit + 1) +
+    I.plan_bytes = static_cast<int64_t>(4 * (slots + (W * P + 1) + nblocks * L.vb + 4 * nseg + nsplit + nsplit + 1) +
                                         2 * nblocks * block_vals);
     p->num_items = static_cast<int32_t>(nseg);
     return RA_OK;
@@ -546,7 +575,7 @@ const ra::DeviceBuffer* plan_array(const ra_tile_plan* p, const std::string& n, 
     const ra_tile_info& I = p->info;
     const int64_t W = I.num_windows;
     elem = 4;
-    if (n == "block_offsets") { count = I.active ? W + 1 : 0; return &p->block_offsets; }
+    if (n == "block_offsets") { count = I.active ? W * std::max(I.col_parts, 1) + 1 : 0; return &p->block_offsets; }
     const int64_t rows = I.rows_per_window > 0 ? I.rows_per_window : ra::kTileWindow;
     const int64_t vb = rows == ra::kTileWindow ? ra::kTileVec : 32;
     if (n == "atox") { count = (int64_t)I.num_blocks * vb; return &p->atox; }

@@ -64,6 +64,10 @@ struct ra_tile_plan {
     int32_t num_items = 0;  // segments (every kind is scheduled as segments)
     ra::DeviceBuffer block_offsets, atox, vals, win_rows, seg_window, seg_bbegin, seg_bend,
         seg_slot, split_windows, split_offsets;
+    // Column partitions (info.col_parts > 1): items and split windows of
+    // partition q are [part_items[q], part_items[q+1]) and
+    // [part_splits[q], part_splits[q+1]); cells are q * num_windows + window.
+    std::vector<int32_t> part_items{0, 0}, part_splits{0, 0};
     ra::DeviceBuffer bconv;    // B converted to fp16/bf16 (grown per K*ldb)
     ra::DeviceBuffer scratch;  // partial slots of split windows
 };

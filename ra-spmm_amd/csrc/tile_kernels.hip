@@ -71,12 +71,27 @@ struct Items {
     const int32_t* seg_bend;
     const int32_t* seg_slot;
     const int32_t* win_rows;       // COMMUNITY_TC
+    int item_base;                 // first segment of this launch
+    int cell_base;                 // partition * windows (column partitions)
+    int accumulate;                // add into C (partitions after the first)
 };
+
+// Write (or, for later column partitions, add) one output value / 16-byte run.
+__device__ __forceinline__ void put1(float* dst, float v, bool add) {
+    if (add) v += *dst;
+    *dst = v;
+}
+template <typename V4>
+__device__ __forceinline__ void put4(float* dst, V4 v, bool add) {
+    if (add) v += *reinterpret_cast<const V4*>(dst);
+    __builtin_nontemporal_store(v, reinterpret_cast<V4*>(dst));
+}
 
 // Work item i = segment i (a whole window unless the window was split).
 __device__ __forceinline__ void item_range(const Items& it, int i, int& w, int& b0, int& b1,
                                            int& slot) {
-    w = static_cast<int>(static_cast<uint32_t>(it.seg_window[i]) & 0x7FFFFFFFu);
+    i += it.item_base;
+    w = static_cast<int>(static_cast<uint32_t>(it.seg_window[i]) & 0x7FFFFFFFu) - it.cell_base;
     b0 = it.seg_bbegin[i];
     b1 = it.seg_bend[i];
     slot = it.seg_slot[i];
@@ -214,19 +229,18 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
         for (int cc = 0; cc < CPL; ++cc) out[cc] = (upper ? acc[cc][2 + k] : acc[cc][k]) * unscale;  // exact
         float* dst = item_row<KIND>(it, C, scratch, w, slot, m, M, N);
         if (!dst) continue;
+        const bool add = it.accumulate && slot < 0;
         if constexpr (CPL % 4 == 0) {
             if (vec) {
 #pragma unroll
-                for (int cc = 0; cc < CPL; cc += 4) {
-                    const f32x4 v = {out[cc], out[cc + 1], out[cc + 2], out[cc + 3]};
-                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst + col + cc));
-                }
+                for (int cc = 0; cc < CPL; cc += 4)
+                    put4(dst + col + cc, f32x4{out[cc], out[cc + 1], out[cc + 2], out[cc + 3]}, add);
                 continue;
             }
         }
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc)
-            if (col + cc < N) dst[col + cc] = out[cc];
+            if (col + cc < N) put1(dst + col + cc, out[cc], add);
     }
 }
 
@@ -326,19 +340,18 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
             float out[CPL];
 #pragma unroll
             for (int cc = 0; cc < CPL; ++cc) out[cc] = acc[g][cc][r] * unscale;  // exact: power of two
+            const bool add = it.accumulate && slot < 0;
             if constexpr (CPL % 4 == 0) {
                 if (vec) {
 #pragma unroll
-                    for (int cc = 0; cc < CPL; cc += 4) {
-                        const f32x4 v = {out[cc], out[cc + 1], out[cc + 2], out[cc + 3]};
-                        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(dst + col + cc));
-                    }
+                    for (int cc = 0; cc < CPL; cc += 4)
+                        put4(dst + col + cc, f32x4{out[cc], out[cc + 1], out[cc + 2], out[cc + 3]}, add);
                     continue;
                 }
             }
 #pragma unroll
             for (int cc = 0; cc < CPL; ++cc)
-                if (col + cc < N) dst[col + cc] = out[cc];
+                if (col + cc < N) put1(dst + col + cc, out[cc], add);
         }
     }
 }
@@ -391,7 +404,7 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_tall_kernel(
 #pragma unroll
     for (int m = 0; m < H; ++m) {
         float* dst = item_row<KIND, H>(it, C, scratch, w, slot, m, M, N);
-        if (dst && col < N) dst[col] = acc[m];
+        if (dst && col < N) put1(dst + col, acc[m], it.accumulate && slot < 0);
     }
 }
 
@@ -464,7 +477,7 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
         if (!dst) continue;
 #pragma unroll
         for (int f = 0; f < F; ++f)
-            if (col + f < N) dst[col + f] = acc[m][f];
+            if (col + f < N) put1(dst + col + f, acc[m][f], it.accumulate && slot < 0);
     }
 }
 
@@ -474,18 +487,19 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
 __global__ __launch_bounds__(kBlock) void tile_merge_kernel(
     const int32_t* __restrict__ split_windows, const int32_t* __restrict__ split_offsets,
     const int32_t* __restrict__ win_rows, const float* __restrict__ scratch, float* __restrict__ C,
-    int M, int N, int H) {
+    int M, int N, int H, int cell_base, int accumulate) {
     const int sw = blockIdx.x;
     const int64_t e = (int64_t)blockIdx.y * kBlock + threadIdx.x;
     if (e >= (int64_t)H * N) return;
     const int m = static_cast<int>(e / N);
     const int n = static_cast<int>(e - (int64_t)m * N);
-    const int64_t slot_row = (int64_t)split_windows[sw] * H + m;
+    const int64_t slot_row = (int64_t)(split_windows[sw] - cell_base) * H + m;
     const int row = win_rows ? win_rows[slot_row] : static_cast<int>(slot_row);
     if (row < 0 || row >= M) return;
     const int o0 = split_offsets[sw], o1 = split_offsets[sw + 1];
     float acc = scratch[((int64_t)o0 * H + m) * N + n];
     for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * H + m) * N + n];
+    if (accumulate) acc = C[(int64_t)row * N + n] + acc;
     C[(int64_t)row * N + n] = acc;
 }
 
@@ -580,8 +594,20 @@ int tile_slice_major(int nslices) {
     return r >= 0 ? r : (nslices >= 4 ? 1 : 0);
 }
 
-Items plan_items(const ra_tile_plan* p) {
+// One launch's share of a plan: all of it, or one column partition.
+struct Part {
+    int item_base, num_items, cell_base, accumulate, split_base, num_splits;
+};
+
+Part whole_plan(const ra_tile_plan* p) {
+    return Part{0, p->num_items, 0, 0, 0, p->info.num_split_windows};
+}
+
+Items plan_items(const ra_tile_plan* p, const Part& part) {
     Items it{};
+    it.item_base = part.item_base;
+    it.cell_base = part.cell_base;
+    it.accumulate = part.accumulate;
     it.block_offsets = p->block_offsets.get<int32_t>();
     it.seg_window = p->seg_window.get<int32_t>();
     it.seg_bbegin = p->seg_bbegin.get<int32_t>();
@@ -592,25 +618,25 @@ Items plan_items(const ra_tile_plan* p) {
 }
 
 template <int KIND>
-ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, bool bf16, float* C,
-                           float* scratch, int N, hipStream_t st) {
+ra_status launch_mfma_kind(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, bool bf16,
+                           float* C, float* scratch, int N, hipStream_t st) {
     const int M = p->info.M;
-    const Items it = plan_items(p);
+    const Items it = plan_items(p, part);
     int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
     cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
     const int remap = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices) ? 2 : 0);
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
-    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
 #define RA_MFMA_CASE(c)                                                                            \
     if (cpl == c) {                                                                                \
         if (bf16)                                                                                  \
             tile_mfma_kernel<c, true, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),    \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale, vec_store); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, part.num_items, nslices, remap, unscale, vec_store); \
         else                                                                                       \
             tile_mfma_kernel<c, false, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),   \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, remap, unscale, vec_store); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, part.num_items, nslices, remap, unscale, vec_store); \
     }
     RA_MFMA_CASE(1)
     RA_MFMA_CASE(2)
@@ -622,15 +648,15 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
 }
 
 template <int KIND>
-ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, float* scratch, int N,
-                           hipStream_t st) {
+ra_status launch_fp32_kind(const ra_tile_plan* p, const Part& part, const float* B, float* C, float* scratch,
+                           int N, hipStream_t st) {
     const int M = p->info.M;
-    const Items it = plan_items(p);
+    const Items it = plan_items(p, part);
     const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
     const bool vec = (N % F == 0) && ((reinterpret_cast<uintptr_t>(B) % (4 * F)) == 0);
     const int nslices = (N + 64 * F - 1) / (64 * F);
     const int remap = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
-    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int bf = p->info.value_dtype == RA_DTYPE_BF16;
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     const int32_t* ax = p->atox.get<int32_t>();
@@ -639,10 +665,10 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
     if (F == f) {                                                                                    \
         if (vec)                                                                                     \
             tile_fp32_kernel<f, true, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch, M, N, \
-                                                                   p->num_items, nslices, remap);   \
+                                                                   part.num_items, nslices, remap);   \
         else                                                                                         \
             tile_fp32_kernel<f, false, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch, M, N, \
-                                                                    p->num_items, nslices, remap);  \
+                                                                    part.num_items, nslices, remap);  \
     }
     RA_FP32_CASE(1)
     RA_FP32_CASE(2)
@@ -652,38 +678,39 @@ ra_status launch_fp32_kind(const ra_tile_plan* p, const float* B, float* C, floa
     return RA_OK;
 }
 
-ra_status launch_merge(const ra_tile_plan* p, float* C, int N, hipStream_t st) {
-    if (p->info.num_split_windows == 0) return RA_OK;
+ra_status launch_merge(const ra_tile_plan* p, const Part& part, float* C, int N, hipStream_t st) {
+    if (part.num_splits == 0) return RA_OK;
     const int H = p->info.rows_per_window;
-    dim3 grid(p->info.num_split_windows, static_cast<unsigned>(((int64_t)H * N + kBlock - 1) / kBlock));
+    dim3 grid(part.num_splits, static_cast<unsigned>(((int64_t)H * N + kBlock - 1) / kBlock));
     const int32_t* wr = p->info.kind == RA_TILE_COMMUNITY_TC ? p->win_rows.get<int32_t>() : nullptr;
-    tile_merge_kernel<<<grid, kBlock, 0, st>>>(p->split_windows.get<int32_t>(),
-                                               p->split_offsets.get<int32_t>(), wr,
-                                               p->scratch.get<float>(), C, p->info.M, N, H);
+    tile_merge_kernel<<<grid, kBlock, 0, st>>>(p->split_windows.get<int32_t>() + part.split_base,
+                                               p->split_offsets.get<int32_t>() + part.split_base, wr,
+                                               p->scratch.get<float>(), C, p->info.M, N, H, part.cell_base,
+                                               part.accumulate);
     RA_LAUNCH_CHECK("tile_merge_kernel");
     return RA_OK;
 }
 
 template <int KIND, int RG>
-ra_status launch_mfma_tall(const ra_tile_plan* p, const uint16_t* Bh, int ldb, bool bf16, float* C,
-                           float* scratch, int N, hipStream_t st) {
+ra_status launch_mfma_tall(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, bool bf16,
+                           float* C, float* scratch, int N, hipStream_t st) {
     const int M = p->info.M;
-    const Items it = plan_items(p);
+    const Items it = plan_items(p, part);
     int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
     cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
     const int order = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices) ? 2 : 0);
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
-    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
 #define RA_TALL_CASE(c)                                                                                  \
     if (cpl == c) {                                                                                      \
         if (bf16)                                                                                        \
             tile_mfma_tall_kernel<c, true, KIND, RG><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(), \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, order, unscale, vec_store); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, part.num_items, nslices, order, unscale, vec_store); \
         else                                                                                             \
             tile_mfma_tall_kernel<c, false, KIND, RG><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(), \
-                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, p->num_items, nslices, order, unscale, vec_store); \
+                p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, part.num_items, nslices, order, unscale, vec_store); \
     }
     RA_TALL_CASE(1)
     RA_TALL_CASE(2)
@@ -695,32 +722,33 @@ ra_status launch_mfma_tall(const ra_tile_plan* p, const uint16_t* Bh, int ldb, b
 }
 
 template <int KIND, int RG>
-ra_status launch_fp32_tall(const ra_tile_plan* p, const float* B, float* C, float* scratch, int N,
-                           hipStream_t st) {
-    const Items it = plan_items(p);
+ra_status launch_fp32_tall(const ra_tile_plan* p, const Part& part, const float* B, float* C, float* scratch,
+                           int N, hipStream_t st) {
+    const Items it = plan_items(p, part);
     const int nslices = (N + 63) / 64;
     const int order = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
-    dim3 grid(static_cast<unsigned>(((int64_t)p->num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     tile_fp32_tall_kernel<KIND, RG><<<grid, kBlock, 0, st>>>(
         it, p->atox.get<int32_t>(), p->vals.get<uint16_t>(), p->info.value_dtype == RA_DTYPE_BF16 ? 1 : 0,
-        std::ldexp(1.0f, -p->info.value_scale_log2), B, C, scratch, p->info.M, N, p->num_items, nslices, order);
+        std::ldexp(1.0f, -p->info.value_scale_log2), B, C, scratch, p->info.M, N, part.num_items, nslices, order);
     RA_LAUNCH_CHECK("tile_fp32_tall_kernel");
     return RA_OK;
 }
 
 template <int KIND>
-ra_status launch_kind(const ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* B32, bool bf16,
-                      bool fp32_route, float* C, float* scratch, int N, hipStream_t st) {
+ra_status launch_kind(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, const float* B32,
+                      bool bf16, bool fp32_route, float* C, float* scratch, int N, hipStream_t st) {
+    if (part.num_items == 0) return RA_OK;
     switch (p->info.rows_per_window) {
         case 16:
-            return fp32_route ? launch_fp32_tall<KIND, 1>(p, B32, C, scratch, N, st)
-                              : launch_mfma_tall<KIND, 1>(p, Bh, ldb, bf16, C, scratch, N, st);
+            return fp32_route ? launch_fp32_tall<KIND, 1>(p, part, B32, C, scratch, N, st)
+                              : launch_mfma_tall<KIND, 1>(p, part, Bh, ldb, bf16, C, scratch, N, st);
         case 32:
-            return fp32_route ? launch_fp32_tall<KIND, 2>(p, B32, C, scratch, N, st)
-                              : launch_mfma_tall<KIND, 2>(p, Bh, ldb, bf16, C, scratch, N, st);
+            return fp32_route ? launch_fp32_tall<KIND, 2>(p, part, B32, C, scratch, N, st)
+                              : launch_mfma_tall<KIND, 2>(p, part, Bh, ldb, bf16, C, scratch, N, st);
         default:
-            return fp32_route ? launch_fp32_kind<KIND>(p, B32, C, scratch, N, st)
-                              : launch_mfma_kind<KIND>(p, Bh, ldb, bf16, C, scratch, N, st);
+            return fp32_route ? launch_fp32_kind<KIND>(p, part, B32, C, scratch, N, st)
+                              : launch_mfma_kind<KIND>(p, part, Bh, ldb, bf16, C, scratch, N, st);
     }
 }
 
@@ -731,18 +759,28 @@ ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* 
         RA_TRY(p->scratch.ensure((size_t)p->info.num_split_segs * p->info.rows_per_window * N * sizeof(float)));
         scratch = p->scratch.get<float>();
     }
-    switch (p->info.kind) {
-        case RA_TILE_TC_DIRECT:
-            RA_TRY(launch_kind<RA_TILE_TC_DIRECT>(p, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
-            break;
-        case RA_TILE_COMMUNITY_TC:
-            RA_TRY(launch_kind<RA_TILE_COMMUNITY_TC>(p, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
-            break;
-        default:
-            RA_TRY(launch_kind<RA_TILE_SEGMENT_HYBRID>(p, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
-            break;
+    // Column partitions run one after another on the stream, each adding into
+    // C what the earlier ones wrote: the per-element sum order is fixed.
+    const int P = std::max(p->info.col_parts, 1);
+    for (int q = 0; q < P; ++q) {
+        const Part part = P == 1 ? whole_plan(p)
+                                 : Part{p->part_items[q], p->part_items[q + 1] - p->part_items[q],
+                                        q * p->info.num_windows, q > 0 ? 1 : 0, p->part_splits[q],
+                                        p->part_splits[q + 1] - p->part_splits[q]};
+        switch (p->info.kind) {
+            case RA_TILE_TC_DIRECT:
+                RA_TRY(launch_kind<RA_TILE_TC_DIRECT>(p, part, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
+                break;
+            case RA_TILE_COMMUNITY_TC:
+                RA_TRY(launch_kind<RA_TILE_COMMUNITY_TC>(p, part, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
+                break;
+            default:
+                RA_TRY(launch_kind<RA_TILE_SEGMENT_HYBRID>(p, part, Bh, ldb, B32, bf16, fp32_route, C, scratch, N,
+                                                           st));
+                break;
+        }
+        RA_TRY(launch_merge(p, part, C, N, st));
     }
-    RA_TRY(launch_merge(p, C, N, st));
     return RA_OK;
 }
 

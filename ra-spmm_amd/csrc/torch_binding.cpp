@@ -477,7 +477,8 @@ void bind_tile_props(pybind11::class_<TilePlan, std::shared_ptr<TilePlan>>& c) {
         .def_property_readonly("max_window_blocks", [](const TilePlan& w) { return w.info.max_window_blocks; })
         .def_property_readonly("num_blocks", [](const TilePlan& w) { return w.info.num_blocks; })
         .def_property_readonly("num_split_segs", [](const TilePlan& w) { return w.info.num_split_segs; })
-        .def_property_readonly("rows_per_window", [](const TilePlan& w) { return w.info.rows_per_window; });
+        .def_property_readonly("rows_per_window", [](const TilePlan& w) { return w.info.rows_per_window; })
+        .def_property_readonly("col_parts", [](const TilePlan& w) { return w.info.col_parts; });
 }
 
 }  // namespace

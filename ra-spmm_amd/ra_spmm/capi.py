@@ -105,7 +105,8 @@ class TileInfo(ctypes.Structure):
         "num_split_windows", "num_split_segs", "max_window_blocks")] + [
         ("nnz", ctypes.c_int64), ("num_vectors", ctypes.c_int64), ("plan_bytes", ctypes.c_int64),
         ("avg_tile_density", ctypes.c_float), ("value_dtype", ctypes.c_int32),
-        ("build_ms", ctypes.c_double), ("value_scale_log2", ctypes.c_int32), ("rows_per_window", ctypes.c_int32)]
+        ("build_ms", ctypes.c_double), ("value_scale_log2", ctypes.c_int32), ("rows_per_window", ctypes.c_int32),
+        ("col_parts", ctypes.c_int32), ("pad3_", ctypes.c_int32)]
 
 
 _lib = None
