@@ -356,10 +356,11 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
     }
 }
 
-// FP32 route on tall windows: one wave per (item, 64-column slice), lane = one
-// column, H accumulators; vectors in ascending column order, exact fp32 FMA of
-// the stored value (as the 8-row FP32 kernel).
-template <int KIND, int RG>
+// FP32 route on tall windows: one wave per (item, column slice, row group of
+// 16); lane covers F consecutive columns (16-byte loads when F = 4 and B is
+// aligned), 16 x F accumulators; vectors in ascending column order, exact fp32
+// FMA of the stored value (as the 8-row FP32 kernel).
+template <int KIND, int RG, int F, bool VEC>
 __global__ __launch_bounds__(kBlock) void tile_fp32_tall_kernel(
     Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
     float unscale, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch,
@@ -368,43 +369,72 @@ __global__ __launch_bounds__(kBlock) void tile_fp32_tall_kernel(
     constexpr int BV = H * 32;
     const int lane = threadIdx.x & (kWave - 1);
     int64_t item_blk;
-    int slice;
-    tile_block_coords(nslices, order, item_blk, slice);
+    int sg;
+    tile_block_coords(nslices * RG, order, item_blk, sg);
+    const int g = sg % RG;
+    const int slice = sg / RG;
     const int item = __builtin_amdgcn_readfirstlane(
         static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
     if (item >= num_items) return;
     int w, b0, b1, slot;
     item_range(it, item, w, b0, b1, slot);
-    const int col = slice * 64 + lane;
-    float acc[H];
+    const int col = slice * (64 * F) + lane * F;
+    float acc[16][F];
 #pragma unroll
-    for (int m = 0; m < H; ++m) acc[m] = 0.f;
+    for (int m = 0; m < 16; ++m)
+#pragma unroll
+        for (int f = 0; f < F; ++f) acc[m][f] = 0.f;
     const bool bf = bf16vals != 0;
     for (int b = b0; b < b1; ++b) {
         for (int v0 = 0; v0 < 32; v0 += 8) {
             int c[8];
-            float bv[8];
+            float bv[8][F];
 #pragma unroll
             for (int v = 0; v < 8; ++v) {
                 c[v] = atox[(int64_t)b * 32 + v0 + v];
-                bv[v] = (c[v] >= 0 && col < N) ? B[(int64_t)c[v] * N + col] : 0.f;
+                if (c[v] >= 0 && col < N) {
+                    const float* src = B + (int64_t)c[v] * N + col;
+                    if constexpr (VEC && F == 4) {
+                        const float4 t = *reinterpret_cast<const float4*>(src);
+                        bv[v][0] = t.x; bv[v][1] = t.y; bv[v][2] = t.z; bv[v][3] = t.w;
+                    } else {
+#pragma unroll
+                        for (int f = 0; f < F; ++f) bv[v][f] = (col + f < N) ? src[f] : 0.f;
+                    }
+                } else {
+#pragma unroll
+                    for (int f = 0; f < F; ++f) bv[v][f] = 0.f;
+                }
             }
+            // Lane L loads row (L & 15)'s 8 values of these vectors (one 16-byte
+            // run, [q = v0/8][j][8]); readlane broadcasts them to every lane.
+            const uint4 run = *reinterpret_cast<const uint4*>(
+                vals + (int64_t)b * BV + ((g * 4 + (v0 >> 3)) * 16 + (lane & 15)) * 8);
+            const uint32_t words[4] = {run.x, run.y, run.z, run.w};
 #pragma unroll
             for (int v = 0; v < 8; ++v) {
                 if (c[v] < 0) break;  // padding sits at the end of the last block
-                const int kk = v0 + v;
 #pragma unroll
-                for (int m = 0; m < H; ++m) {
-                    const uint16_t s = vals[(int64_t)b * BV + (((m >> 4) * 4 + (kk >> 3)) * 16 + (m & 15)) * 8 + (kk & 7)];
-                    acc[m] = __builtin_fmaf(stored_to_f32(s, bf) * unscale, bv[v], acc[m]);
+                for (int m = 0; m < 16; ++m) {
+                    const uint32_t word = __builtin_amdgcn_readlane(words[v >> 1], m);
+                    const uint16_t h = static_cast<uint16_t>((v & 1) ? (word >> 16) : (word & 0xFFFFu));
+                    // Wave-uniform: a tall block is mostly zeros, skip them.
+                    if ((h & 0x7FFFu) == 0) continue;
+                    const float a = stored_to_f32(h, bf) * unscale;  // exact
+#pragma unroll
+                    for (int f = 0; f < F; ++f) acc[m][f] = __builtin_fmaf(a, bv[v][f], acc[m][f]);
                 }
             }
         }
     }
+    const bool add = it.accumulate && slot < 0;
 #pragma unroll
-    for (int m = 0; m < H; ++m) {
-        float* dst = item_row<KIND, H>(it, C, scratch, w, slot, m, M, N);
-        if (dst && col < N) put1(dst + col, acc[m], it.accumulate && slot < 0);
+    for (int m = 0; m < 16; ++m) {
+        float* dst = item_row<KIND, H>(it, C, scratch, w, slot, 16 * g + m, M, N);
+        if (!dst) continue;
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+            if (col + f < N) put1(dst + col + f, acc[m][f], add);
     }
 }
 
@@ -725,12 +755,27 @@ template <int KIND, int RG>
 ra_status launch_fp32_tall(const ra_tile_plan* p, const Part& part, const float* B, float* C, float* scratch,
                            int N, hipStream_t st) {
     const Items it = plan_items(p, part);
-    const int nslices = (N + 63) / 64;
+    const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
+    const bool vec = F == 4 && (N % 4 == 0) && ra::aligned16(B);
+    const int nslices = (N + 64 * F - 1) / (64 * F);
     const int order = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
-    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
-    tile_fp32_tall_kernel<KIND, RG><<<grid, kBlock, 0, st>>>(
-        it, p->atox.get<int32_t>(), p->vals.get<uint16_t>(), p->info.value_dtype == RA_DTYPE_BF16 ? 1 : 0,
-        std::ldexp(1.0f, -p->info.value_scale_log2), B, C, scratch, p->info.M, N, part.num_items, nslices, order);
+    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices * RG));
+    const int bf = p->info.value_dtype == RA_DTYPE_BF16 ? 1 : 0;
+    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
+    const int32_t* ax = p->atox.get<int32_t>();
+    const uint16_t* vl = p->vals.get<uint16_t>();
+    if (F == 1)
+        tile_fp32_tall_kernel<KIND, RG, 1, false><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
+                                                                         p->info.M, N, part.num_items, nslices, order);
+    else if (F == 2)
+        tile_fp32_tall_kernel<KIND, RG, 2, false><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
+                                                                         p->info.M, N, part.num_items, nslices, order);
+    else if (vec)
+        tile_fp32_tall_kernel<KIND, RG, 4, true><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
+                                                                        p->info.M, N, part.num_items, nslices, order);
+    else
+        tile_fp32_tall_kernel<KIND, RG, 4, false><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
+                                                                         p->info.M, N, part.num_items, nslices, order);
     RA_LAUNCH_CHECK("tile_fp32_tall_kernel");
     return RA_OK;
 }
