@@ -352,6 +352,9 @@ torch::Tensor run_zero_overhead_plan(std::shared_ptr<ZOPlan> w, torch::Tensor ro
     check_gpu_tensor(vals, "vals");
     check_dense_float(B, "B");
     TORCH_CHECK(w && w->valid, "Invalid ZeroOverhead plan");
+    TORCH_CHECK(B.size(0) >= w->info.K, "B has ", B.size(0), " rows; the plan was built for K = ", w->info.K);
+    TORCH_CHECK(rowptr.numel() == w->info.M + 1, "rowptr has ", rowptr.numel(), " entries; the plan was built for M = ",
+                w->info.M);
     TORCH_CHECK(rowptr.scalar_type() == torch::kInt32 && colind.scalar_type() == torch::kInt32 &&
                     vals.scalar_type() == torch::kFloat32,
                 "rowptr/colind must be int32 and vals float32");
@@ -372,6 +375,8 @@ void run_zero_overhead_plan_stage(std::shared_ptr<ZOPlan> w, torch::Tensor rowpt
     TORCH_CHECK(w && w->valid, "Invalid ZeroOverhead plan");
     check_dense_float(B, "B");
     check_dense_float(C, "C");
+    TORCH_CHECK(B.size(0) >= w->info.K, "B has ", B.size(0), " rows; the plan was built for K = ", w->info.K);
+    TORCH_CHECK(rowptr.numel() == w->info.M + 1, "rowptr does not match the plan's M");
     TORCH_CHECK(C.size(0) == w->info.M && C.size(1) == B.size(1), "C must be [M, N]");
     check(ra_zo_plan_run_stage(w->plan, rowptr.data_ptr<int32_t>(), colind.data_ptr<int32_t>(),
                                vals.data_ptr<float>(), B.data_ptr<float>(), C.data_ptr<float>(),
@@ -436,6 +441,7 @@ torch::Tensor run_tile_plan(const std::shared_ptr<TilePlan>& w, const torch::Ten
     TORCH_CHECK(w && w->valid, "Invalid tile plan");
     check_gpu_tensor(B, "B");
     TORCH_CHECK(B.dim() == 2, "B must be 2-D");
+    TORCH_CHECK(B.size(0) >= w->info.K, "B has ", B.size(0), " rows; the plan was built for K = ", w->info.K);
     const int M = w->info.M;
     const int N = static_cast<int>(B.size(1));
     auto C = torch::empty({M, N}, B.options().dtype(torch::kFloat32));

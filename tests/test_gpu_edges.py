@@ -78,3 +78,18 @@ def test_one_long_row(oracle):
     for name, C in _all_paths(rp, ci, vl, 1, K, B).items():
         tol = 2.0 ** -10 if name in ("tc", "comm", "seg") else 1e-5
         assert np.all(np.abs(C.cpu().numpy() - ref) <= tol * scale), name
+
+
+def test_B_with_too_few_rows_is_rejected():
+    """A B shorter than the plan's K would make the gathers read past B: the
+    plan runs refuse it instead of launching."""
+    from ra_spmm import synthetic as S
+    g = S.random_csr(100, 80, 6.0, seed=1)
+    rp, ci, vl = g.torch("cuda")
+    short = torch.randn(40, 32, device="cuda")
+    z = ra_spmm.make_zero_overhead_plan(rp, g.M, g.K)
+    with pytest.raises(RuntimeError, match="rows"):
+        ra_spmm.run_zero_overhead_plan(z, rp, ci, vl, short)
+    t = ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, 32)
+    with pytest.raises(RuntimeError, match="rows"):
+        ra_spmm.run_tc_direct_plan(t, short)
