@@ -451,9 +451,12 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
 
     // Sort nonzeros by (cell, column, slot), stable in CSR position.
     const int64_t NC = W * P;
+    if (NC >= INT32_MAX)
+        return ra::fail(RA_ERR_UNSUPPORTED, "tile: too many windows x column partitions for int32 cell ids");
     int wbits = 0;
     while ((int64_t(1) << wbits) < NC) ++wbits;
     const int wshift = 31 + L.sb;
+    if (wshift + wbits > 64) return ra::fail(RA_ERR_UNSUPPORTED, "tile: sort key wider than 64 bits");
     if (n > 0) {
         entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, L.sb, cols_per_part, W,
                                                      keys, idx);
