@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Routed SpMM benchmark on one MI355X (driver contract: one JSON line on stdout).
 
-Default workload = BASELINE config 2: Chung-Lu power-law graph (M = 1e6, mean
+Default workload = config C2: Chung-Lu power-law graph (M = 1e6, mean
 degree 16, gamma 2.1, hubs), GCN-normalised fp32 values, dense B of 1e6 x 128
 fp32 N(0,1) (synthetic, seeded), C = A @ B through the MI355X router.
 
@@ -230,7 +230,7 @@ def profile_traffic(kernel: str, cfg: str, N: int):
 
 
 def bench_gcn(steps, warmup, table, backends=("router", "cusparse", "zero_overhead", "csr_direct")):
-    """2-layer GCN training step (128 -> 256 -> 47) on the
+    """config C5: 2-layer GCN training step (128 -> 256 -> 47) on the
     synthetic power-law operator, forward A X and backward A^T G routed per
     (transpose, N).  Reports step time per backend and the routed paths."""
     import numpy as np

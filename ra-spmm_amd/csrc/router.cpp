@@ -57,7 +57,7 @@ constexpr RouterTable kReference = {
     0, 0, 1e30f, 0};
 
 // MI355X calibration (structure of the tree unchanged; measured on gfx950 with
-// bench.py --sweep over the five BASELINE configs):
+// bench.py --sweep over the five benchmark configs C1-C5):
 //  - tile gate: the device tile build (sorts and scans on the GPU) runs at
 //    1.1-1.8e-10 s per nnz (C2 1.6e7 nnz: 2.8 ms; C4 1.24e8 nnz: 13.5 ms),
 //    plus ~3e-10 s per nnz to upload a host CSR (the host builder took

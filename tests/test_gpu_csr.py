@@ -133,7 +133,7 @@ def test_capi_csr_direct_direct_call(oracle):
 
 
 def test_c2_full_size_properties(oracle):
-    """BASELINE config 2 at full size: bit-exact against the oracle on a row
+    """config C2 at full size: bit-exact against the oracle on a row
     sample, linearity in B and the all-ones row-sum identity on every row."""
     g = S.CONFIGS["C2"]()
     rp, ci, vl = _dev(g)

@@ -134,7 +134,7 @@ def test_inactive_plan_raises_and_families_agree(oracle):
 
 
 def test_c3_full_size_properties(oracle):
-    """BASELINE config 3 (SBM, fp16 values) at full size through TC_DIRECT and
+    """config C3 (SBM, fp16 values) at full size through TC_DIRECT and
     COMMUNITY_TC: a row sample against the oracle, and all-ones row sums."""
     g = S.CONFIGS["C3"]()
     gd = g.torch("cuda")
