@@ -494,14 +494,42 @@ def tile_decode(fmt, M, K):
     return A
 
 
+def merge_duplicates(rowptr, colind, vals):
+    """CSR with repeated (row, column) entries summed in fp32, in CSR order
+    (0 + v0 + v1 + ...), the first occurrence keeping its position: what a
+    tile plan stores before rounding (tc/ra_tc_direct.cu:654-706 writes every
+    duplicate into one fragment slot; the plan here sums them).  Pinned in
+    tests/test_oracle_structures.py against a dense accumulation."""
+    rowptr = np.asarray(rowptr, dtype=np.int64)
+    colind = np.asarray(colind, dtype=np.int64)
+    vals = np.asarray(vals, dtype=np.float32)
+    M = len(rowptr) - 1
+    out_rp, out_ci, out_v = [0], [], []
+    for r in range(M):
+        seen = {}
+        for p in range(int(rowptr[r]), int(rowptr[r + 1])):
+            c = int(colind[p])
+            if c in seen:
+                out_v[seen[c]] = np.float32(out_v[seen[c]] + vals[p])
+            else:
+                seen[c] = len(out_v)
+                out_ci.append(c)
+                out_v.append(np.float32(np.float32(0.0) + vals[p]))
+        out_rp.append(len(out_ci))
+    return (np.array(out_rp, dtype=np.int32), np.array(out_ci, dtype=np.int32),
+            np.array(out_v, dtype=np.float32))
+
+
 def spmm_tile_f64(rowptr, colind, vals, B, route: str):
     """Exact value of a tile path's output: vals quantised like the plan
     (fp16 with the plan's power-of-two scale for F16 and FP32 routes, bf16 for
     BF16), B quantised like the route
     (fp16 / bf16 / unchanged), fp64 accumulation.  The reference FP16 path
     computes the same products exactly (fp16 x fp16 is exact in fp32) and
-    differs only in fp32 summation order (tc/ra_tc_direct.cu:109-179)."""
-    sc = tile_value_scale_log2(vals)
+    differs only in fp32 summation order (tc/ra_tc_direct.cu:109-179).
+    Duplicate (row, column) entries are summed first (merge_duplicates)."""
+    sc = tile_value_scale_log2(vals)  # from the stored entries, before merging
+    rowptr, colind, vals = merge_duplicates(rowptr, colind, vals)
     if route == "f16":
         qv, qb = quantize_f16_scaled(vals, sc), quantize_f16(B)
     elif route == "bf16":

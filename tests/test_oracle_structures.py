@@ -199,3 +199,27 @@ def test_segments_cover_windows(kind, limit):
         assert all(a[1] == b[0] for a, b in zip(pieces, pieces[1:]))
     assert info.num_split_windows == len(h["split_windows"]) > 0
     assert h["split_offsets"][-1] == info.num_split_segs
+
+
+def test_merge_duplicates_matches_dense_accumulation(oracle):
+    rng = np.random.default_rng(5)
+    M, K = 40, 12
+    deg = rng.integers(0, 9, M)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, K, rp[-1]).astype(np.int32)
+    vl = rng.standard_normal(rp[-1]).astype(np.float32)
+    mrp, mci, mvl = oracle.merge_duplicates(rp, ci, vl)
+    dense = np.zeros((M, K), np.float64)
+    np.add.at(dense, (np.repeat(np.arange(M), deg), ci), vl.astype(np.float64))
+    got = np.zeros((M, K), np.float64)
+    np.add.at(got, (np.repeat(np.arange(M), np.diff(mrp)), mci), mvl.astype(np.float64))
+    np.testing.assert_allclose(got, dense, rtol=1e-6, atol=1e-6)
+    for r in range(M):                      # distinct columns per row, first-occurrence order
+        row = mci[mrp[r]:mrp[r + 1]]
+        assert len(set(row.tolist())) == len(row)
+        first = list(dict.fromkeys(ci[rp[r]:rp[r + 1]].tolist()))
+        assert row.tolist() == first
+    # fp32 accumulation in CSR order: three equal entries of 1 + 2^-24 sum exactly as float32 does
+    v = np.float32(1 + 2 ** -23)
+    _, _, s = oracle.merge_duplicates(np.array([0, 3]), np.array([0, 0, 0]), np.array([v, v, v], np.float32))
+    assert s[0] == np.float32(np.float32(np.float32(v + v)) + v)
