@@ -612,16 +612,18 @@ int tile_max_cpl() {
     return c;
 }
 
-// RA_TILE_SLICE_MAJOR: 1 = always, 0 = never; unset = when the row is split
-// into 4 or more slices (N > 384), where the whole-row working set is 4x the
-// slice's (C4 N=512: 16.9 -> 16.0 ms; at 2 slices the re-read A stream cancels
-// the gain).
-int tile_slice_major(int nslices) {
+// RA_TILE_SLICE_MAJOR: 1 = always, 0 = never; unset = with the XCD window
+// remap on and the row split into 4 or more slices (N > 384), where the
+// whole-row working set is 4x the slice's.  Measured on C4 N=512 with 8 column
+// partitions: TC_DIRECT (remapped) 14.4 -> 9.5 ms with slice-major order;
+// COMMUNITY_TC (never remapped) 9.85 -> 8.94 ms without it.  At 2 slices the
+// re-read A stream cancels the gain.
+int tile_slice_major(int nslices, bool remapped) {
     static const int r = [] {
         const char* e = std::getenv("RA_TILE_SLICE_MAJOR");
         return e ? (std::atoi(e) != 0 ? 1 : 0) : -1;
     }();
-    return r >= 0 ? r : (nslices >= 4 ? 1 : 0);
+    return r >= 0 ? r : (nslices >= 4 && remapped ? 1 : 0);
 }
 
 // One launch's share of a plan: all of it, or one column partition.
@@ -655,7 +657,7 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const Part& part, const uint16
     int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
     cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
-    const int remap = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices) ? 2 : 0);
+    const int remap = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices, KIND != RA_TILE_COMMUNITY_TC && tile_remap()) ? 2 : 0);
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
@@ -729,7 +731,7 @@ ra_status launch_mfma_tall(const ra_tile_plan* p, const Part& part, const uint16
     int cpl = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8;
     cpl = std::min(cpl, tile_max_cpl());
     const int nslices = (N + 16 * cpl - 1) / (16 * cpl);
-    const int order = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices) ? 2 : 0);
+    const int order = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) | (tile_slice_major(nslices, KIND != RA_TILE_COMMUNITY_TC && tile_remap()) ? 2 : 0);
     const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
     dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
     const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
