@@ -127,7 +127,8 @@ def quantize_f16(x) -> np.ndarray:
     """IEEE fp16 round-to-nearest-even, returned as fp32 (numpy's conversion is
     the library routine; reference host_float_to_half_bits, tc/ra_tc_direct.cu:45-69,
     and __float2half_rn in tc/ra_community_tc.cu:34-39 are both RNE)."""
-    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):  # beyond 65504 rounds to inf, as RNE does
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
 def tile_value_scale_log2(vals) -> int:
