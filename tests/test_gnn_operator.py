@@ -49,3 +49,31 @@ def test_cross_entropy_matches_torch():
     ga, = torch.autograd.grad(a, logits)
     gb, = torch.autograd.grad(b, logits)
     torch.testing.assert_close(ga, gb, rtol=1e-6, atol=1e-7)
+
+
+def test_chunked_weight_grad_and_linear(monkeypatch):
+    import torch
+    from ra_spmm import gnn
+    g = torch.randn(1000, 5, dtype=torch.float64)
+    x = torch.randn(1000, 3, dtype=torch.float64)
+    ref = g.t() @ x
+    for rows in (7, 64, 250):  # with and without a remainder; c >= 4 chunks
+        torch.testing.assert_close(gnn.weight_grad(g, x, rows), ref)
+    torch.testing.assert_close(gnn.weight_grad(g[:20], x[:20], 7), g[:20].t() @ x[:20])  # < 4 chunks: one GEMM
+    # Same parameters as nn.Linear(bias=False) from the same seed; gradients
+    # of the chunked form equal autograd's through F.linear.
+    monkeypatch.setattr(gnn, "WGRAD_ROWS", 16)
+    torch.manual_seed(3)
+    lin = gnn.Linear(3, 5).double()
+    torch.manual_seed(3)
+    ref_lin = torch.nn.Linear(3, 5, bias=False).double()
+    torch.testing.assert_close(lin.weight, ref_lin.weight)
+    xi = x.clone().requires_grad_(True)
+    xr = x.clone().requires_grad_(True)
+    out = lin(xi)
+    assert out.shape == (1000, 8) and bool((out[:, 5:] == 0).all())  # width padded to a multiple of 4
+    torch.testing.assert_close(out[:, :5], ref_lin(xr))
+    (out[:, :5] ** 2).sum().backward()
+    (ref_lin(xr) ** 2).sum().backward()
+    torch.testing.assert_close(lin.weight.grad, ref_lin.weight.grad)
+    torch.testing.assert_close(xi.grad, xr.grad)

@@ -49,8 +49,8 @@ def test_gcn_step_matches_dense_reference():
         results[backend] = (out.detach(), [p.grad.detach().clone() for p in model.parameters()], fp16)
     torch.manual_seed(1)
     ref_model = gnn.GCN(32, 64, 7).cuda()
-    h = F.relu(dense @ ref_model.lin1(X))
-    ref_out = dense @ ref_model.lin2(h)
+    h = F.relu(dense @ F.linear(X, ref_model.lin1.weight))
+    ref_out = dense @ F.linear(h, ref_model.lin2.weight)
     F.cross_entropy(ref_out, y).backward()
     ref_grads = [p.grad for p in ref_model.parameters()]
     for backend, (out, grads, fp16) in results.items():
@@ -103,3 +103,16 @@ def test_padded_narrow_width_is_exact(oracle):
     np.testing.assert_array_equal(got[short], ref[short])
     scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B.cpu().numpy()))
     assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-30)
+
+
+def test_chunked_weight_grad_on_device():
+    """The GCN's weight gradient over 300k rows (36 chunks + a remainder) against
+    fp64: the chunked sum is held to 1e-5 of sum |g||x|."""
+    torch.manual_seed(5)
+    for out_f, in_f in ((256, 128), (47, 256)):
+        g = torch.randn(300_001, out_f, device="cuda")
+        x = torch.randn(300_001, in_f, device="cuda")
+        got = gnn.weight_grad(g, x).double()
+        ref = g.double().t() @ x.double()
+        scale = g.double().abs().t() @ x.double().abs()
+        assert float(((got - ref).abs() / scale).max()) < 1e-5
