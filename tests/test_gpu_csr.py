@@ -214,3 +214,30 @@ def test_zero_overhead_run_device_plan_equals_host_plan():
     dev = ra_spmm.make_zero_overhead_plan(rp, g.M, g.K)
     assert torch.equal(ra_spmm.run_zero_overhead_plan(host, rp, ci, vl, B),
                        ra_spmm.run_zero_overhead_plan(dev, rp, ci, vl, B))
+
+
+def test_c5_full_size_routed_widths(oracle):
+    """config C5 (GCN operator of a 1e6-row power-law graph) at the GCN's
+    widths 256 and 48 through the routed path: rows of at most 64 nonzeros
+    bit-exact against the sequential fp32 oracle, longer rows (split into
+    chunks) within 1e-5 of fp64, on a row sample with the 50 longest rows."""
+    g = S.CONFIGS["C5"]()
+    rp, ci, vl = _dev(g)
+    deg = np.diff(g.rowptr)
+    rows = np.unique(np.concatenate([np.arange(0, g.M, 1999), np.argsort(deg)[-50:]]))
+    sub_rp = np.concatenate([[0], np.cumsum(deg[rows])]).astype(np.int32)
+    sub_ci = np.concatenate([g.colind[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    sub_vl = np.concatenate([g.vals[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    short = deg[rows] <= 64
+    for N in (256, 48):
+        print(f"[c5 full] N={N}", flush=True)
+        plan_dict = ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N)
+        label = ra_spmm.route_label(plan_dict)
+        assert label == "ZERO_OVERHEAD_CSR", label
+        plan = ra_spmm.build_kernel_plan(label, rp.cpu(), ci.cpu(), vl.cpu(), g.M, g.K, N)
+        Bn = _B(g.K, N, 50 + N)
+        C = ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, torch.from_numpy(Bn).cuda()).cpu().numpy()[rows]
+        seq = oracle.spmm_seq_f32(sub_rp, sub_ci, sub_vl, Bn)
+        np.testing.assert_array_equal(C[short], seq[short])
+        assert_close_scaled(C, oracle.spmm_f64(sub_rp, sub_ci, sub_vl, Bn),
+                            oracle.spmm_f64(sub_rp, sub_ci, np.abs(sub_vl), np.abs(Bn)), 1e-5, f"C5 N={N}")

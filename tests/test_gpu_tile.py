@@ -159,3 +159,37 @@ def test_c3_full_size_properties(oracle):
         exact[deg == 0] = 0
         assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
         del plan
+
+
+def test_c4_full_size_properties(oracle):
+    """config C4 (log-normal degrees to 20k, fp16 values) at full size through
+    the routed COMMUNITY_TC and TC_DIRECT with the automatic 8 column
+    partitions: a row sample (including the 20 longest rows) against the
+    oracle at N=512, and the all-ones row sums on every row."""
+    g = S.CONFIGS["C4"]()
+    gd = g.torch("cuda")
+    N = 512
+    rng = np.random.default_rng(4)
+    B = rng.standard_normal((g.K, N)).astype(np.float16).astype(np.float32)
+    Bd = torch.from_numpy(B).cuda()
+    deg = np.diff(g.rowptr)
+    rows = np.unique(np.concatenate([np.arange(0, g.M, 2003), np.argsort(deg)[-20:]]))
+    sub_rp = np.concatenate([[0], np.cumsum(deg[rows])]).astype(np.int32)
+    sub_ci = np.concatenate([g.colind[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    sub_vl = np.concatenate([g.vals[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    ref = oracle.spmm_f64(sub_rp, sub_ci, sub_vl, B)
+    scale = oracle.spmm_f64(sub_rp, sub_ci, np.abs(sub_vl), np.abs(B))
+    exact = np.add.reduceat(np.append(g.vals.astype(np.float64), 0), g.rowptr[:-1])
+    exact[deg == 0] = 0
+    for kind in (1, 0):
+        print(f"[c4 full] kind={kind}", flush=True)
+        plan = MAKE[kind](gd[0], gd[1], gd[2], g.M, g.K, N)
+        assert plan.col_parts == 8 and plan.rows_per_window == 8
+        C = run(kind, plan, Bd, "f16", gd)
+        assert_close_scaled(C.cpu().numpy()[rows], ref, scale, 1e-5, f"C4 kind {kind}")
+        del C
+        ones = torch.ones(g.K, 16, device="cuda")
+        rs = run(kind, plan, ones, "f16", gd)[:, 0].double().cpu().numpy()
+        assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
+        del plan
+        torch.cuda.empty_cache()
