@@ -48,6 +48,11 @@ void check_csr(const torch::Tensor& rowptr, const torch::Tensor& colind, const t
 void check_same_device(const torch::Tensor& a, const torch::Tensor& b) {
     TORCH_CHECK(a.device() == b.device(), "tensors must be on the same device");
 }
+// Plans hold device memory of the GPU they were built on.
+void check_plan_device(int plan_device, const torch::Tensor& B) {
+    TORCH_CHECK(B.device().index() == plan_device, "the plan was built on cuda:", plan_device, ", B is on ",
+                B.device());
+}
 
 torch::Tensor host_i32(const torch::Tensor& t) { return t.cpu().contiguous().to(torch::kInt32); }
 torch::Tensor host_f32(const torch::Tensor& t) { return t.cpu().contiguous().to(torch::kFloat32); }
@@ -58,6 +63,7 @@ torch::Tensor spmm_csr_direct(torch::Tensor rowptr, torch::Tensor colind, torch:
     check_csr(rowptr, colind, vals);
     check_dense_float(B, "B");
     check_same_device(rowptr, B);
+    const c10::DeviceGuard guard(B.device());
     const int M = static_cast<int>(rowptr.size(0)) - 1;
     const int K = static_cast<int>(B.size(0));
     const int N = static_cast<int>(B.size(1));
@@ -75,6 +81,7 @@ torch::Tensor spmm_csr_baseline(torch::Tensor rowptr, torch::Tensor colind, torc
     check_csr(rowptr, colind, vals);
     check_dense_float(B, "B");
     check_same_device(rowptr, B);
+    const c10::DeviceGuard guard(B.device());
     const int M = static_cast<int>(rowptr.size(0)) - 1;
     const int K = static_cast<int>(B.size(0));
     const int N = static_cast<int>(B.size(1));
@@ -98,6 +105,7 @@ std::shared_ptr<BaselinePlan> make_cusparse_plan(torch::Tensor rowptr, torch::Te
                                                  torch::Tensor vals, torch::Tensor B) {
     check_csr(rowptr, colind, vals);
     check_dense_float(B, "B");
+    check_same_device(rowptr, B);
     auto p = std::make_shared<BaselinePlan>();
     p->rowptr = rowptr;
     p->colind = colind;
@@ -113,6 +121,8 @@ torch::Tensor run_cusparse_plan(std::shared_ptr<BaselinePlan> p, torch::Tensor B
     check_dense_float(B, "B");
     TORCH_CHECK(B.size(0) == p->K && B.size(1) == p->N, "cuSPARSE plan expects B shape [", p->K,
                 ", ", p->N, "], got [", B.size(0), ", ", B.size(1), "]");
+    check_same_device(p->C, B);
+    const c10::DeviceGuard guard(B.device());
     const int M = static_cast<int>(p->rowptr.size(0)) - 1;
     check(ra_spmm_csr_baseline(p->rowptr.data_ptr<int32_t>(), p->colind.data_ptr<int32_t>(),
                                p->vals.data_ptr<float>(), B.data_ptr<float>(),
@@ -129,6 +139,7 @@ ra_features features_of(const torch::Tensor& rowptr, int M, int K, int N, const 
     if (rowptr.is_cuda()) {
         TORCH_CHECK(rowptr.scalar_type() == torch::kInt32 && rowptr.is_contiguous(),
                     "device rowptr must be contiguous int32");
+        const c10::DeviceGuard guard(rowptr.device());
         check(ra_features_device(rowptr.data_ptr<int32_t>(), M, K, N, current_stream(), &f),
               "features");
         *backend = "cuda_rowptr_moments";
@@ -319,6 +330,7 @@ struct ZOPlan {
     ra_zo_plan* plan = nullptr;
     ra_zo_info info{};
     bool valid = false;
+    int device = -1;
     ~ZOPlan() { ra_zo_plan_destroy(plan); }
 };
 
@@ -332,10 +344,13 @@ std::shared_ptr<ZOPlan> make_zero_overhead_plan(torch::Tensor rowptr_cpu, int M,
     auto w = std::make_shared<ZOPlan>();
     if (build == "host") {
         auto rp = host_i32(rowptr_cpu);
+        w->device = c10::hip::current_device();
         check(ra_zo_plan_create(rp.data_ptr<int32_t>(), M, K, &w->plan), "make_zero_overhead_plan");
     } else {
         const auto dev = rowptr_cpu.is_cuda() ? rowptr_cpu.device()
                                               : torch::Device(torch::kCUDA, c10::hip::current_device());
+        const c10::DeviceGuard guard(dev);
+        w->device = dev.index();
         auto rp = rowptr_cpu.to(torch::TensorOptions().device(dev).dtype(torch::kInt32)).contiguous();
         check(ra_zo_plan_create_device(rp.data_ptr<int32_t>(), M, K, current_stream(), &w->plan),
               "make_zero_overhead_plan");
@@ -358,6 +373,9 @@ torch::Tensor run_zero_overhead_plan(std::shared_ptr<ZOPlan> w, torch::Tensor ro
     TORCH_CHECK(rowptr.scalar_type() == torch::kInt32 && colind.scalar_type() == torch::kInt32 &&
                     vals.scalar_type() == torch::kFloat32,
                 "rowptr/colind must be int32 and vals float32");
+    check_same_device(rowptr, B);
+    check_plan_device(w->device, B);
+    const c10::DeviceGuard guard(B.device());
     const int M = w->info.M;
     const int N = static_cast<int>(B.size(1));
     auto C = torch::empty({M, N}, B.options());
@@ -373,8 +391,13 @@ void run_zero_overhead_plan_stage(std::shared_ptr<ZOPlan> w, torch::Tensor rowpt
                                   torch::Tensor colind, torch::Tensor vals, torch::Tensor B,
                                   torch::Tensor C, int stage) {
     TORCH_CHECK(w && w->valid, "Invalid ZeroOverhead plan");
+    check_csr(rowptr, colind, vals);
     check_dense_float(B, "B");
     check_dense_float(C, "C");
+    check_same_device(rowptr, B);
+    check_same_device(C, B);
+    check_plan_device(w->device, B);
+    const c10::DeviceGuard guard(B.device());
     TORCH_CHECK(B.size(0) >= w->info.K, "B has ", B.size(0), " rows; the plan was built for K = ", w->info.K);
     TORCH_CHECK(rowptr.numel() == w->info.M + 1, "rowptr does not match the plan's M");
     TORCH_CHECK(C.size(0) == w->info.M && C.size(1) == B.size(1), "C must be [M, N]");
@@ -389,6 +412,7 @@ struct TilePlan {
     ra_tile_plan* plan = nullptr;
     ra_tile_info info{};
     bool valid = false;
+    int device = -1;
     ~TilePlan() { ra_tile_plan_destroy(plan); }
 };
 
@@ -416,12 +440,15 @@ std::shared_ptr<TilePlan> make_tile_plan(int kind, torch::Tensor rowptr_cpu, tor
         auto rp = host_i32(rowptr_cpu);
         auto ci = host_i32(colind_cpu);
         auto vl = host_f32(vals_cpu);
+        w->device = c10::hip::current_device();
         check(ra_tile_plan_create(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
                                   vl.data_ptr<float>(), M, K, N, vd, &w->plan),
               what);
     } else {
         const auto dev = rowptr_cpu.is_cuda() ? rowptr_cpu.device()
                                               : torch::Device(torch::kCUDA, c10::hip::current_device());
+        const c10::DeviceGuard guard(dev);
+        w->device = dev.index();
         auto opts = torch::TensorOptions().device(dev);
         auto rp = rowptr_cpu.to(opts.dtype(torch::kInt32)).contiguous();
         auto ci = colind_cpu.to(opts.dtype(torch::kInt32)).contiguous();
@@ -442,6 +469,8 @@ torch::Tensor run_tile_plan(const std::shared_ptr<TilePlan>& w, const torch::Ten
     check_gpu_tensor(B, "B");
     TORCH_CHECK(B.dim() == 2, "B must be 2-D");
     TORCH_CHECK(B.size(0) >= w->info.K, "B has ", B.size(0), " rows; the plan was built for K = ", w->info.K);
+    check_plan_device(w->device, B);
+    const c10::DeviceGuard guard(B.device());
     const int M = w->info.M;
     const int N = static_cast<int>(B.size(1));
     auto C = torch::empty({M, N}, B.options().dtype(torch::kFloat32));
