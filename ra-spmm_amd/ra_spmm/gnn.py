@@ -143,10 +143,12 @@ class GraphBackend:
                 tmpl = torch.empty((M, int(ncols)), device=self.device, dtype=torch.float32)
                 ex = (label, _C.make_cusparse_plan(t["rowptr"], t["colind"], t["vals"], tmpl))
             else:
-                # Tile plans are N-independent (N only gates N >= 16): share one
-                # plan per (family, transpose) across widths and precisions.
+                # Tile plans (N only gates N >= 16) and ZERO_OVERHEAD_CSR plans
+                # (a partial buffer that grows to the widest N) do not depend
+                # on N: share one plan per (family, transpose) across widths
+                # and precisions.
                 plan = None
-                if label in TILE_KERNELS:
+                if label in TILE_KERNELS or label == "ZERO_OVERHEAD_CSR":
                     fam = label.replace("_TF32", "")
                     for (b, tr, n), (lab, p) in self.exec_cache.items():
                         if tr == transpose and lab.replace("_TF32", "") == fam and p is not None:

@@ -80,6 +80,23 @@ def test_router_plans_per_transpose_and_width():
         assert dt > 0
 
 
+def test_zero_overhead_plan_shared_across_widths():
+    """One ZERO_OVERHEAD_CSR plan per transpose serves every width (its
+    partial buffer grows to the widest); results stay exact against dense."""
+    op = _operator(4000, seed=9)
+    graph = gnn.GraphBackend(op, "cuda")
+    dense = torch.from_numpy(op.toarray()).cuda()
+    for n in (48, 256, 16, 256):
+        for t in (False, True):
+            B = torch.randn(op.shape[0], n, device="cuda")
+            out = graph.run(B, "zero_overhead", transpose=t)
+            ref = (dense.t() if t else dense) @ B
+            torch.testing.assert_close(out, ref, rtol=1e-4, atol=1e-5)
+    for t in (False, True):
+        plans = {id(p) for (b, tr, n), (lab, p) in graph.exec_cache.items() if tr == t}
+        assert len(plans) == 1
+
+
 def test_padded_narrow_width_is_exact(oracle):
     """Widths not divisible by 4 run on a zero-padded copy in the CSR family.
     CSR_DIRECT keeps its fma chain per element: bit-identical to the unpadded
