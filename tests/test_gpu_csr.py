@@ -33,6 +33,9 @@ CASES = [
     (257, 300, 5.0, 0.0, 0.1, 16),
     (1000, 800, 9.0, 1.3, 0.05, 32),
     (1000, 1000, 12.0, 1.1, 0.0, 47),     # ragged N: scalar packets
+    (1003, 900, 11.0, 1.2, 0.02, 48),     # 12 float4 packets in 16-lane groups
+    (999, 700, 7.0, 0.8, 0.05, 36),       # 9 packets
+    (1001, 800, 9.0, 1.0, 0.0, 44),       # 11 packets
     (2048, 1500, 20.0, 1.2, 0.02, 64),
     (3000, 2000, 16.0, 1.05, 0.01, 128),
     (1500, 1500, 30.0, 1.5, 0.0, 256),
@@ -69,7 +72,7 @@ def test_csr_direct_unaligned_B_uses_scalar_path(oracle):
     np.testing.assert_array_equal(C.cpu().numpy(), oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B))
 
 
-@pytest.mark.parametrize("N", [32, 47, 64, 128, 256, 512])
+@pytest.mark.parametrize("N", [32, 36, 44, 47, 48, 64, 128, 256, 512])
 def test_zero_overhead_hub_rows(oracle, N):
     print(f"[zo] N={N}", flush=True)
     # Power-law rows: tiny/short/medium/long bins plus multi-chunk hubs.
