@@ -321,7 +321,11 @@ ra_status ra_tile_plan_create_device(int32_t kind, const int32_t* d_rowptr, cons
 ra_status ra_tile_plan_export(const ra_tile_plan* plan, const char* name, void* dst,
                               int64_t* count);
 /* B fp32 [K,N]; route: ra_tile_route.  The FP16/BF16 routes convert B into
- * plan scratch first (one extra pass over B). */
+ * plan scratch first (one extra pass over B).  RA_TILE_ROUTE_FP32 (the
+ * reference's TF32 route, tc/ra_tc_direct.cu:805-894) computes exact fp32 fma
+ * of the stored values as a CSR SpMM: its first call derives that CSR from the
+ * plan on the device (allocates and synchronises `stream` once), later calls
+ * only launch. */
 ra_status ra_tile_plan_run(ra_tile_plan* plan, const float* d_B, float* d_C, int32_t N,
                            int32_t route, ra_stream_t stream);
 /* B already fp16/bf16 with leading dimension ldb (elements, ldb >= N and a

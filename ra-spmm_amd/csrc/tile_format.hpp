@@ -70,4 +70,22 @@ struct ra_tile_plan {
     std::vector<int32_t> part_items{0, 0}, part_splits{0, 0};
     ra::DeviceBuffer bconv;    // B converted to fp16/bf16 (grown per K*ldb)
     ra::DeviceBuffer scratch;  // partial slots of split windows
+    // FP32 route: the stored values as a CSR sorted by (row, column), derived
+    // on the first FP32-route call (tile_f32_route.hip), and a
+    // ZERO_OVERHEAD_CSR plan over it when the row lengths are skewed.
+    bool f32_ready = false;
+    int64_t f32_nnz = 0;
+    ra::DeviceBuffer f32_rowptr, f32_colind, f32_vals;
+    ra_zo_plan* f32_zo = nullptr;
+    ra_tile_plan() = default;
+    ra_tile_plan(const ra_tile_plan&) = delete;
+    ra_tile_plan& operator=(const ra_tile_plan&) = delete;
+    ~ra_tile_plan() { ra_zo_plan_destroy(f32_zo); }
 };
+
+namespace ra {
+// FP32 route of a tile plan: derive the CSR of the stored values once, then
+// run CSR_DIRECT (or ZERO_OVERHEAD_CSR for skewed rows) on it.
+ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st);
+ra_status tile_f32_run(ra_tile_plan* p, const float* B, float* C, int32_t N, hipStream_t st);
+}  // namespace ra

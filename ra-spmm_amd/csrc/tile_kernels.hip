@@ -13,10 +13,10 @@
 //   - feeds block b+q as the A fragment in block-diagonal form: rows 0-7 of the
 //     16-row MFMA carry blocks b, b+1 and rows 8-15 carry b+2, b+3, so an 8-row
 //     window fills the 16x16x32 shape; the two halves are summed at the end.
-// FP32 route (tile_fp32_kernel): replaces the reference's TF32 path (gfx950 has
-// no xf32 MFMA): one wavefront per (item, column slice), B read in fp32, exact
-// fp32 FMA of the stored fp16/bf16 value times B, vectors in ascending column
-// order.
+// FP32 route (the `_tf32` entry points): replaces the reference's TF32 path
+// (gfx950 has no xf32 MFMA) with exact fp32 FMA of the stored fp16/bf16 values
+// and fp32 B, run as a CSR SpMM over the plan's stored values
+// (tile_f32_route.hip).
 //
 // Reference: fs_tile_spmm[_staged]_kernel tc/ra_tc_direct.cu:109-179, 270-328;
 //            ct_fs_tile_spmm_perm_kernel tc/ra_community_tc.cu:106-190;
@@ -244,10 +244,6 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     }
 }
 
-__device__ __forceinline__ float stored_to_f32(uint16_t h, bool bf16) {
-    if (bf16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
-    return static_cast<float>(__builtin_bit_cast(_Float16, h));
-}
 
 // ------------------------------------------------- MFMA route, tall windows
 // Windows of H = 16*RG rows; a block is 32 vectors (one MFMA K) with values
@@ -353,161 +349,6 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
             for (int cc = 0; cc < CPL; ++cc)
                 if (col + cc < N) put1(dst + col + cc, out[cc], add);
         }
-    }
-}
-
-// FP32 route on tall windows: one wave per (item, column slice, row group of
-// 16); lane covers F consecutive columns (16-byte loads when F = 4 and B is
-// aligned), 16 x F accumulators; vectors in ascending column order, exact fp32
-// FMA of the stored value (as the 8-row FP32 kernel).
-template <int KIND, int RG, int F, bool VEC>
-__global__ __launch_bounds__(kBlock) void tile_fp32_tall_kernel(
-    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
-    float unscale, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch,
-    int M, int N, int num_items, int nslices, int order) {
-    constexpr int H = 16 * RG;
-    constexpr int BV = H * 32;
-    const int lane = threadIdx.x & (kWave - 1);
-    int64_t item_blk;
-    int sg;
-    tile_block_coords(nslices * RG, order, item_blk, sg);
-    const int g = sg % RG;
-    const int slice = sg / RG;
-    const int item = __builtin_amdgcn_readfirstlane(
-        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
-    if (item >= num_items) return;
-    int w, b0, b1, slot;
-    item_range(it, item, w, b0, b1, slot);
-    const int col = slice * (64 * F) + lane * F;
-    float acc[16][F];
-#pragma unroll
-    for (int m = 0; m < 16; ++m)
-#pragma unroll
-        for (int f = 0; f < F; ++f) acc[m][f] = 0.f;
-    const bool bf = bf16vals != 0;
-    for (int b = b0; b < b1; ++b) {
-        for (int v0 = 0; v0 < 32; v0 += 8) {
-            int c[8];
-            float bv[8][F];
-#pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                c[v] = atox[(int64_t)b * 32 + v0 + v];
-                if (c[v] >= 0 && col < N) {
-                    const float* src = B + (int64_t)c[v] * N + col;
-                    if constexpr (VEC && F == 4) {
-                        const float4 t = *reinterpret_cast<const float4*>(src);
-                        bv[v][0] = t.x; bv[v][1] = t.y; bv[v][2] = t.z; bv[v][3] = t.w;
-                    } else {
-#pragma unroll
-                        for (int f = 0; f < F; ++f) bv[v][f] = (col + f < N) ? src[f] : 0.f;
-                    }
-                } else {
-#pragma unroll
-                    for (int f = 0; f < F; ++f) bv[v][f] = 0.f;
-                }
-            }
-            // Lane L loads row (L & 15)'s 8 values of these vectors (one 16-byte
-            // run, [q = v0/8][j][8]); readlane broadcasts them to every lane.
-            const uint4 run = *reinterpret_cast<const uint4*>(
-                vals + (int64_t)b * BV + ((g * 4 + (v0 >> 3)) * 16 + (lane & 15)) * 8);
-            const uint32_t words[4] = {run.x, run.y, run.z, run.w};
-#pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                if (c[v] < 0) break;  // padding sits at the end of the last block
-#pragma unroll
-                for (int m = 0; m < 16; ++m) {
-                    const uint32_t word = __builtin_amdgcn_readlane(words[v >> 1], m);
-                    const uint16_t h = static_cast<uint16_t>((v & 1) ? (word >> 16) : (word & 0xFFFFu));
-                    // Wave-uniform: a tall block is mostly zeros, skip them.
-                    if ((h & 0x7FFFu) == 0) continue;
-                    const float a = stored_to_f32(h, bf) * unscale;  // exact
-#pragma unroll
-                    for (int f = 0; f < F; ++f) acc[m][f] = __builtin_fmaf(a, bv[v][f], acc[m][f]);
-                }
-            }
-        }
-    }
-    const bool add = it.accumulate && slot < 0;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-        float* dst = item_row<KIND, H>(it, C, scratch, w, slot, 16 * g + m, M, N);
-        if (!dst) continue;
-#pragma unroll
-        for (int f = 0; f < F; ++f)
-            if (col + f < N) put1(dst + col + f, acc[m][f], add);
-    }
-}
-
-// ------------------------------------------------------------ FP32 route
-
-// One wavefront per (item, slice of 64*F columns); lane covers F consecutive
-// columns.  VEC: F-wide vector loads/stores (needs N % F == 0 and alignment).
-template <int F, bool VEC, int KIND>
-__global__ __launch_bounds__(kBlock) void tile_fp32_kernel(
-    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals, int bf16vals,
-    float unscale, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ scratch,
-    int M, int N, int num_items, int nslices, int remap) {
-    const int lane = threadIdx.x & (kWave - 1);
-    int64_t item_blk;
-    int slice;
-    tile_block_coords(nslices, remap, item_blk, slice);
-    const int item = __builtin_amdgcn_readfirstlane(
-        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
-    if (item >= num_items) return;
-    int w, b0, b1, slot;
-    item_range(it, item, w, b0, b1, slot);
-    const int col = slice * (64 * F) + lane * F;
-    float acc[8][F];
-#pragma unroll
-    for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int f = 0; f < F; ++f) acc[r][f] = 0.f;
-    const bool bf = bf16vals != 0;
-    for (int b = b0; b < b1; ++b) {
-        // All 8 indices of the block first (wave-uniform), then all 8 gathers,
-        // then the FMAs in vector (= ascending column) order.
-        int c[8];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) c[v] = atox[(int64_t)b * 8 + v];
-        float bv[8][F];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-            if (c[v] >= 0 && col < N) {
-                const float* src = B + (int64_t)c[v] * N + col;
-                if constexpr (VEC && F == 4) {
-                    const float4 t = *reinterpret_cast<const float4*>(src);
-                    bv[v][0] = t.x; bv[v][1] = t.y; bv[v][2] = t.z; bv[v][3] = t.w;
-                } else if constexpr (VEC && F == 2) {
-                    const float2 t = *reinterpret_cast<const float2*>(src);
-                    bv[v][0] = t.x; bv[v][1] = t.y;
-                } else {
-#pragma unroll
-                    for (int f = 0; f < F; ++f) bv[v][f] = (col + f < N) ? src[f] : 0.f;
-                }
-            } else {
-#pragma unroll
-                for (int f = 0; f < F; ++f) bv[v][f] = 0.f;
-            }
-        }
-        const uint16_t* vb = vals + (int64_t)b * 64;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-            if (c[v] < 0) break;  // padding sits at the end of the last block
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const float a = stored_to_f32(vb[r * 8 + v], bf) * unscale;  // exact
-#pragma unroll
-                for (int f = 0; f < F; ++f) acc[r][f] = __builtin_fmaf(a, bv[v][f], acc[r][f]);
-            }
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        float* dst = item_row<KIND>(it, C, scratch, w, slot, m, M, N);
-        if (!dst) continue;
-#pragma unroll
-        for (int f = 0; f < F; ++f)
-            if (col + f < N) put1(dst + col + f, acc[m][f], it.accumulate && slot < 0);
     }
 }
 
@@ -679,37 +520,6 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const Part& part, const uint16
     return RA_OK;
 }
 
-template <int KIND>
-ra_status launch_fp32_kind(const ra_tile_plan* p, const Part& part, const float* B, float* C, float* scratch,
-                           int N, hipStream_t st) {
-    const int M = p->info.M;
-    const Items it = plan_items(p, part);
-    const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
-    const bool vec = (N % F == 0) && ((reinterpret_cast<uintptr_t>(B) % (4 * F)) == 0);
-    const int nslices = (N + 64 * F - 1) / (64 * F);
-    const int remap = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
-    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
-    const int bf = p->info.value_dtype == RA_DTYPE_BF16;
-    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
-    const int32_t* ax = p->atox.get<int32_t>();
-    const uint16_t* vl = p->vals.get<uint16_t>();
-#define RA_FP32_CASE(f)                                                                              \
-    if (F == f) {                                                                                    \
-        if (vec)                                                                                     \
-            tile_fp32_kernel<f, true, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch, M, N, \
-                                                                   part.num_items, nslices, remap);   \
-        else                                                                                         \
-            tile_fp32_kernel<f, false, KIND><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch, M, N, \
-                                                                    part.num_items, nslices, remap);  \
-    }
-    RA_FP32_CASE(1)
-    RA_FP32_CASE(2)
-    RA_FP32_CASE(4)
-#undef RA_FP32_CASE
-    RA_LAUNCH_CHECK("tile_fp32_kernel");
-    return RA_OK;
-}
-
 ra_status launch_merge(const ra_tile_plan* p, const Part& part, float* C, int N, hipStream_t st) {
     if (part.num_splits == 0) return RA_OK;
     const int H = p->info.rows_per_window;
@@ -753,54 +563,22 @@ ra_status launch_mfma_tall(const ra_tile_plan* p, const Part& part, const uint16
     return RA_OK;
 }
 
-template <int KIND, int RG>
-ra_status launch_fp32_tall(const ra_tile_plan* p, const Part& part, const float* B, float* C, float* scratch,
-                           int N, hipStream_t st) {
-    const Items it = plan_items(p, part);
-    const int F = N <= 64 ? 1 : N <= 128 ? 2 : 4;
-    const bool vec = F == 4 && (N % 4 == 0) && ra::aligned16(B);
-    const int nslices = (N + 64 * F - 1) / (64 * F);
-    const int order = KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap();
-    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices * RG));
-    const int bf = p->info.value_dtype == RA_DTYPE_BF16 ? 1 : 0;
-    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
-    const int32_t* ax = p->atox.get<int32_t>();
-    const uint16_t* vl = p->vals.get<uint16_t>();
-    if (F == 1)
-        tile_fp32_tall_kernel<KIND, RG, 1, false><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
-                                                                         p->info.M, N, part.num_items, nslices, order);
-    else if (F == 2)
-        tile_fp32_tall_kernel<KIND, RG, 2, false><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
-                                                                         p->info.M, N, part.num_items, nslices, order);
-    else if (vec)
-        tile_fp32_tall_kernel<KIND, RG, 4, true><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
-                                                                        p->info.M, N, part.num_items, nslices, order);
-    else
-        tile_fp32_tall_kernel<KIND, RG, 4, false><<<grid, kBlock, 0, st>>>(it, ax, vl, bf, unscale, B, C, scratch,
-                                                                         p->info.M, N, part.num_items, nslices, order);
-    RA_LAUNCH_CHECK("tile_fp32_tall_kernel");
-    return RA_OK;
-}
-
 template <int KIND>
-ra_status launch_kind(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, const float* B32,
-                      bool bf16, bool fp32_route, float* C, float* scratch, int N, hipStream_t st) {
+ra_status launch_kind(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, bool bf16, float* C,
+                      float* scratch, int N, hipStream_t st) {
     if (part.num_items == 0) return RA_OK;
     switch (p->info.rows_per_window) {
         case 16:
-            return fp32_route ? launch_fp32_tall<KIND, 1>(p, part, B32, C, scratch, N, st)
-                              : launch_mfma_tall<KIND, 1>(p, part, Bh, ldb, bf16, C, scratch, N, st);
+            return launch_mfma_tall<KIND, 1>(p, part, Bh, ldb, bf16, C, scratch, N, st);
         case 32:
-            return fp32_route ? launch_fp32_tall<KIND, 2>(p, part, B32, C, scratch, N, st)
-                              : launch_mfma_tall<KIND, 2>(p, part, Bh, ldb, bf16, C, scratch, N, st);
+            return launch_mfma_tall<KIND, 2>(p, part, Bh, ldb, bf16, C, scratch, N, st);
         default:
-            return fp32_route ? launch_fp32_kind<KIND>(p, part, B32, C, scratch, N, st)
-                              : launch_mfma_kind<KIND>(p, part, Bh, ldb, bf16, C, scratch, N, st);
+            return launch_mfma_kind<KIND>(p, part, Bh, ldb, bf16, C, scratch, N, st);
     }
 }
 
-ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* B32, bool bf16,
-                     bool fp32_route, float* C, int N, hipStream_t st) {
+// FP16/BF16 MFMA route over 16-bit B (converted, or passed in by the caller).
+ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, bool bf16, float* C, int N, hipStream_t st) {
     float* scratch = nullptr;
     if (p->info.num_split_segs > 0) {
         RA_TRY(p->scratch.ensure((size_t)p->info.num_split_segs * p->info.rows_per_window * N * sizeof(float)));
@@ -816,14 +594,13 @@ ra_status run_common(ra_tile_plan* p, const uint16_t* Bh, int ldb, const float* 
                                         p->part_splits[q + 1] - p->part_splits[q]};
         switch (p->info.kind) {
             case RA_TILE_TC_DIRECT:
-                RA_TRY(launch_kind<RA_TILE_TC_DIRECT>(p, part, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
+                RA_TRY(launch_kind<RA_TILE_TC_DIRECT>(p, part, Bh, ldb, bf16, C, scratch, N, st));
                 break;
             case RA_TILE_COMMUNITY_TC:
-                RA_TRY(launch_kind<RA_TILE_COMMUNITY_TC>(p, part, Bh, ldb, B32, bf16, fp32_route, C, scratch, N, st));
+                RA_TRY(launch_kind<RA_TILE_COMMUNITY_TC>(p, part, Bh, ldb, bf16, C, scratch, N, st));
                 break;
             default:
-                RA_TRY(launch_kind<RA_TILE_SEGMENT_HYBRID>(p, part, Bh, ldb, B32, bf16, fp32_route, C, scratch, N,
-                                                           st));
+                RA_TRY(launch_kind<RA_TILE_SEGMENT_HYBRID>(p, part, Bh, ldb, bf16, C, scratch, N, st));
                 break;
         }
         RA_TRY(launch_merge(p, part, C, N, st));
@@ -892,7 +669,7 @@ ra_status ra_tile_plan_run(ra_tile_plan* p, const float* d_B, float* d_C, int32_
     if (N <= 0 || p->info.M == 0) return RA_OK;
     if (!d_B || !d_C) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: NULL B or C");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (route == RA_TILE_ROUTE_FP32) return run_common(p, nullptr, 0, d_B, false, true, d_C, N, st);
+    if (route == RA_TILE_ROUTE_FP32) return ra::tile_f32_run(p, d_B, d_C, N, st);
     if (route != RA_TILE_ROUTE_F16 && route != RA_TILE_ROUTE_BF16)
         return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: unknown route");
     const bool bf16 = route == RA_TILE_ROUTE_BF16;
@@ -901,7 +678,7 @@ ra_status ra_tile_plan_run(ra_tile_plan* p, const float* d_B, float* d_C, int32_
     const int ldb = (N + 7) / 8 * 8;
     RA_TRY(p->bconv.ensure((size_t)p->info.K * ldb * sizeof(uint16_t)));
     RA_TRY(launch_convert(d_B, p->bconv.get(), p->info.K, N, ldb, bf16, st));
-    return run_common(p, p->bconv.get<uint16_t>(), ldb, nullptr, bf16, false, d_C, N, st);
+    return run_common(p, p->bconv.get<uint16_t>(), ldb, bf16, d_C, N, st);
 }
 
 ra_status ra_tile_plan_run_lowp(ra_tile_plan* p, const void* d_Bh, int32_t ldb, int32_t b_dtype,
@@ -917,8 +694,7 @@ ra_status ra_tile_plan_run_lowp(ra_tile_plan* p, const void* d_Bh, int32_t ldb, 
     if (b_dtype != RA_DTYPE_F16 && !bf16) return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: b_dtype must be F16 or BF16");
     if (bf16 != (p->info.value_dtype == RA_DTYPE_BF16))
         return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: B precision differs from the plan's value dtype");
-    return run_common(p, static_cast<const uint16_t*>(d_Bh), ldb, nullptr, bf16, false, d_C, N,
-                      reinterpret_cast<hipStream_t>(stream));
+    return run_common(p, static_cast<const uint16_t*>(d_Bh), ldb, bf16, d_C, N, reinterpret_cast<hipStream_t>(stream));
 }
 
 ra_status ra_tile_plan_get_info(const ra_tile_plan* p, ra_tile_info* info) {

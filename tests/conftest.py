@@ -37,3 +37,31 @@ def assert_close_scaled(C, C64, scale, rel, what=""):
         raise AssertionError(
             f"{what}: {int(bad.sum())} elements beyond rel={rel}; first at {tuple(i)}: "
             f"got {C[tuple(i)]!r}, exact {C64[tuple(i)]!r}, bound {bound[tuple(i)]!r}")
+
+
+def assert_fp32_route(C32, rowptr, colind, vals, B, oracle, what="fp32 route"):
+    """The tile plans' FP32 route (the `_tf32` entry points) against the oracle.
+
+    rowptr/colind/vals is the CSR a plan stores: duplicates merged, values
+    rounded and scaled back (oracle.merge_duplicates, quantize_f16_scaled).
+    The route drops stored zeros and runs CSR_DIRECT, one fp32 fma chain per
+    element in ascending column order: bit-identical to oracle.spmm_seq_f32.
+    When the row lengths are skewed (population CV >= 1.5) it runs
+    ZERO_OVERHEAD_CSR: rows of <= 64 stored nonzeros stay bit-identical, longer
+    rows are held to 1e-5 of |A||B|."""
+    rowptr = np.asarray(rowptr, np.int64)
+    colind, vals = np.asarray(colind), np.asarray(vals)
+    rows = np.repeat(np.arange(rowptr.size - 1), np.diff(rowptr))
+    order = np.lexsort((colind, rows))  # ascending columns within each row
+    colind, vals = colind[order], vals[order]
+    keep = vals != 0
+    deg = np.add.reduceat(np.append(keep.astype(np.int64), 0), rowptr[:-1]) * (np.diff(rowptr) > 0)
+    seq = oracle.spmm_seq_f32(rowptr.astype(np.int32), colind, vals, B)
+    cv = deg.std() / deg.mean() if deg.size and deg.mean() > 0 else 0.0
+    if cv < 1.5:
+        np.testing.assert_array_equal(C32, seq, err_msg=what)
+        return
+    short = deg <= 64
+    np.testing.assert_array_equal(np.asarray(C32)[short], seq[short], err_msg=what)
+    assert_close_scaled(C32, oracle.spmm_f64(rowptr.astype(np.int32), colind, vals, B),
+                        oracle.spmm_f64(rowptr.astype(np.int32), colind, np.abs(vals), np.abs(B)), 1e-5, what)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_scaled
+from conftest import assert_close_scaled, assert_fp32_route
 
 pytestmark = pytest.mark.gpu
 
@@ -74,9 +74,8 @@ def test_random_parity(oracle, seed):
                                 oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5,
                                 f"tile f16 kind={kind} rows={p.rows_per_window} parts={p.col_parts}")
             C32 = ra_spmm.run_tile_plan_route(p, Bd, "fp32").cpu().numpy()
-            assert_close_scaled(C32, oracle.spmm_f64(mrp, mci, qs, B),
-                                oracle.spmm_f64(mrp, mci, np.abs(qs), np.abs(B)), 1e-5,
-                                f"tile fp32 kind={kind} rows={p.rows_per_window} parts={p.col_parts}")
+            assert_fp32_route(C32, mrp, mci, qs, B, oracle,
+                              f"tile fp32 kind={kind} rows={p.rows_per_window} parts={p.col_parts}")
     finally:
         if old is None:
             del os.environ["RA_TILE_COL_PARTS"]

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_scaled
+from conftest import assert_close_scaled, assert_fp32_route
 
 pytestmark = pytest.mark.gpu
 
@@ -60,8 +60,7 @@ def test_partitioned_routes(oracle, gname, kind, parts, rows):
                         oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5, "parts f16")
     qs = oracle.quantize_f16_scaled(g.vals, oracle.tile_value_scale_log2(g.vals))
     C32 = ra_spmm.run_tile_plan_route(plan, Bd, "fp32").cpu().numpy()
-    assert_close_scaled(C32, oracle.spmm_f64(g.rowptr, g.colind, qs, B),
-                        oracle.spmm_f64(g.rowptr, g.colind, np.abs(qs), np.abs(B)), 1e-5, "parts fp32")
+    assert_fp32_route(C32, g.rowptr, g.colind, qs, B, oracle, f"parts fp32 parts={parts} rows={rows}")
     np.testing.assert_array_equal(ra_spmm.run_tile_plan_route(plan, Bd, "fp16").cpu().numpy(), C)
 
 

@@ -2,16 +2,15 @@
 decodes back to the matrix (values rounded and scaled as in the 8-row format),
 and the MFMA / FP32 routes meet the 8-row format's bars:
   FP16 / BF16 route  vs fp64 of the quantised inputs: 1e-5 (scaled by |A||B|);
-  FP32 route         bit-identical to the sequential fp32 fma chain over the
-                     stored values when no window is split (vectors ascend in
-                     column order within each row), else 1e-5.
+  FP32 route         the CSR of the stored values, as for 8-row plans
+                     (conftest.assert_fp32_route).
 The automatic height picks a tall layout where rows of a window share columns
 (community graphs) and keeps 8 rows where they do not."""
 import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_scaled
+from conftest import assert_close_scaled, assert_fp32_route
 
 pytestmark = pytest.mark.gpu
 
@@ -88,11 +87,7 @@ def test_tall_routes(oracle, gname, kind, rows, N):
                         oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5, "tall f16")
     C32 = ra_spmm.run_tile_plan_route(plan, Bd, "fp32").cpu().numpy()
     qs = oracle.quantize_f16_scaled(g.vals, oracle.tile_value_scale_log2(g.vals))
-    if plan.num_split_windows > 0:
-        assert_close_scaled(C32, oracle.spmm_f64(g.rowptr, g.colind, qs, B),
-                            oracle.spmm_f64(g.rowptr, g.colind, np.abs(qs), np.abs(B)), 1e-5, "tall fp32 split")
-    else:
-        np.testing.assert_array_equal(C32, oracle.spmm_seq_f32(g.rowptr, g.colind, qs, B))
+    assert_fp32_route(C32, g.rowptr, g.colind, qs, B, oracle, f"tall fp32 {gname} kind={kind} rows={rows}")
     np.testing.assert_array_equal(ra_spmm.run_tile_plan_route(plan, Bd, "fp16").cpu().numpy(), C)
 
 
