@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kBlock) void csr_rows_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
     const float* __restrict__ vals, const P* __restrict__ Bp, P* __restrict__ Cp,
     const int32_t* __restrict__ row_list, int64_t num_rows, int64_t ldp, int np, int remap,
-    int nt) {
+    int nt, int resume) {
     constexpr int RPW = kWave / G;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -150,9 +150,12 @@ __global__ __launch_bounds__(kBlock) void csr_rows_kernel(
         const int qq = q0 + sl + s * G;
         q[s] = qq < np ? qq : -1;
     }
+    // resume: the fma chain continues from C (a later column range of the same
+    // rows; storing and reloading the fp32 accumulator changes no bit).
     P acc[V];
 #pragma unroll
-    for (int s = 0; s < V; ++s) acc[s] = pzero<P>();
+    for (int s = 0; s < V; ++s)
+        acc[s] = (resume && q[s] >= 0) ? Cp[(int64_t)row * ldp + q[s]] : pzero<P>();
     accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, rowptr[row], rowptr[row + 1], sl, q, acc,
                                  nt != 0);
 #pragma unroll
@@ -434,13 +437,13 @@ LaneShape pick_shape(int np, int packet_elems) {
 template <typename P>
 ra_status launch_csr_rows(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_t* rowptr,
                           const int32_t* colind, const float* vals, const P* B, P* C,
-                          const int32_t* row_list, int64_t num_rows, int64_t ldp, int np) {
+                          const int32_t* row_list, int64_t num_rows, int64_t ldp, int np, int resume) {
     const int remap = tuning().remap, nt = tuning().nt;
 #define RA_ROWS_CASE(g, v, u)                                                               \
     if (sh.G == g && sh.V == v && sh.U == u) {                                              \
         csr_rows_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(rowptr, colind, vals, B, C,    \
                                                              row_list, num_rows, ldp, np,   \
-                                                             remap, nt);                    \
+                                                             remap, nt, resume);            \
         RA_LAUNCH_CHECK("csr_rows_kernel");                                                 \
         return RA_OK;                                                                       \
     }
@@ -506,14 +509,13 @@ ra_status check_spmm_args(const void* rowptr, const void* colind, const void* va
 
 // ============================================================ ZO plan object
 
-extern "C" {
+namespace ra {
 
-ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
-                             const float* d_vals, const float* d_B, float* d_C, int32_t M,
-                             int32_t K, int32_t N, int64_t nnz, ra_stream_t stream) {
+ra_status csr_direct_launch(const int32_t* d_rowptr, const int32_t* d_colind, const float* d_vals,
+                            const float* d_B, float* d_C, int32_t M, int32_t K, int32_t N, int64_t nnz,
+                            bool resume, hipStream_t st) {
     RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals, d_B, d_C, M, K, N, nnz));
     if (M == 0 || N == 0) return RA_OK;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
     const int np = vec ? N / 4 : N;
     const LaneShape sh = pick_shape(np, vec ? 4 : 1);
@@ -522,9 +524,20 @@ ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
     if (vec)
         return launch_csr_rows<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
                                        reinterpret_cast<const float4*>(d_B),
-                                       reinterpret_cast<float4*>(d_C), nullptr, M, np, np);
+                                       reinterpret_cast<float4*>(d_C), nullptr, M, np, np, resume ? 1 : 0);
     return launch_csr_rows<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
-                                  nullptr, M, np, np);
+                                  nullptr, M, np, np, resume ? 1 : 0);
+}
+
+}  // namespace ra
+
+extern "C" {
+
+ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
+                             const float* d_vals, const float* d_B, float* d_C, int32_t M,
+                             int32_t K, int32_t N, int64_t nnz, ra_stream_t stream) {
+    return ra::csr_direct_launch(d_rowptr, d_colind, d_vals, d_B, d_C, M, K, N, nnz, false,
+                                 reinterpret_cast<hipStream_t>(stream));
 }
 
 ra_status ra_spmm_csr_baseline(const int32_t* d_rowptr, const int32_t* d_colind,

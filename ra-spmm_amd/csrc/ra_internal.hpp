@@ -113,4 +113,11 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // hardware_concurrency threads (plan builders; no OpenMP runtime needed).
 void parallel_for(int64_t n, int64_t grain, const std::function<void(int64_t, int64_t)>& f);
 
+// CSR_DIRECT launch (csr_kernels.hip).  resume = the fma chain of every output
+// element continues from the value in C instead of 0 (C then holds the chain
+// over an earlier column range of the same rows).
+ra_status csr_direct_launch(const int32_t* d_rowptr, const int32_t* d_colind, const float* d_vals,
+                            const float* d_B, float* d_C, int32_t M, int32_t K, int32_t N, int64_t nnz,
+                            bool resume, hipStream_t st);
+
 }  // namespace ra

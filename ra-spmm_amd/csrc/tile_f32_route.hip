@@ -15,13 +15,16 @@
 //   4. rowptr from the last index of each row and a max-scan (no atomics)
 // and keeps (rowptr, colind, vals).  Every later call runs CSR_DIRECT on them:
 // one fp32 fma chain per output element in ascending column order, the same
-// chain the tile kernels computed, bit for bit.  Rows of skewed length
+// chain the tile kernels computed, bit for bit.  A plan with column partitions
+// keeps them: one CSR per column range, launched in order, each continuing
+// the chains the previous one left in C (the B rows in use stay K / P).  Rows of skewed length
 // (degree CV >= 1.5, the router's own ZERO_OVERHEAD_CSR threshold) run on a
 // ZERO_OVERHEAD_CSR plan instead, which keeps rows of <= 64 nonzeros
 // bit-exact and sums longer rows in 256-nonzero chunks.
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 
 #include "ra_internal.hpp"
@@ -66,12 +69,15 @@ __device__ __forceinline__ int64_t cell_of(const int32_t* __restrict__ boff, int
 
 // Pass 1: nonzero stored values of every vector.  Pass 2 (emit): their keys
 // and values at the vector's offset.
+// With column partitions kept (parts > 1) the key's row is part * M + row, so
+// the sorted CSR holds partition 0's rows, then partition 1's, ...
 template <bool EMIT>
 __global__ void vector_entries(const int32_t* __restrict__ boff, int64_t ncells, int64_t W,
                                const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
                                const int32_t* __restrict__ win_rows, int64_t nvec, int H, int vb, int bf16,
-                               float unscale, int32_t* __restrict__ count, const int32_t* __restrict__ offset,
-                               uint64_t* __restrict__ keys, float* __restrict__ out) {
+                               float unscale, int parts, int64_t M, int32_t* __restrict__ count,
+                               const int32_t* __restrict__ offset, uint64_t* __restrict__ keys,
+                               float* __restrict__ out) {
     RA_GRID_STRIDE(v, nvec) {
         const int32_t col = atox[v];
         int n = 0;
@@ -79,13 +85,17 @@ __global__ void vector_entries(const int32_t* __restrict__ boff, int64_t ncells,
             const int64_t b = v / vb;
             const int kk = static_cast<int>(v - b * vb);
             int64_t o = EMIT ? offset[v] : 0;
-            int64_t w = 0;
-            if (EMIT) w = cell_of(boff, ncells, b) % W;
+            int64_t w = 0, part = 0;
+            if (EMIT) {
+                const int64_t cell = cell_of(boff, ncells, b);
+                w = cell % W;
+                part = parts > 1 ? cell / W : 0;
+            }
             for (int slot = 0; slot < H; ++slot) {
                 const uint16_t h = vals[value_at(b, slot, kk, H, vb)];
                 if ((h & 0x7FFFu) == 0) continue;  // +0 / -0: no product
                 if (EMIT) {
-                    const int32_t row = win_rows[w * H + slot];
+                    const int64_t row = part * M + win_rows[w * H + slot];
                     keys[o] = (static_cast<uint64_t>(row) << 31) | static_cast<uint32_t>(col);
                     out[o] = stored_value(h, bf16 != 0, unscale);
                     ++o;
@@ -129,6 +139,17 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
     const int64_t nvec = (int64_t)I.num_blocks * vb;
     const float unscale = std::ldexp(1.0f, -I.value_scale_log2);
     const int bf16 = I.value_dtype == RA_DTYPE_BF16 ? 1 : 0;
+    // Column partitions of the plan are kept (one CSR per column range, run in
+    // order) when the (part * M + row, column) key fits 64 bits.
+    int parts = std::max(I.col_parts, 1);
+    int rbits = 1;
+    while ((int64_t(1) << rbits) < (int64_t)parts * M) ++rbits;
+    if (31 + rbits > 64 || (int64_t)parts * M >= INT32_MAX) {
+        parts = 1;
+        rbits = 1;
+        while ((int64_t(1) << rbits) < M) ++rbits;
+    }
+    const int64_t R = (int64_t)parts * M;  // rows of the derived CSR
 
     // Per-vector counts and their exclusive scan (nvec + 1 entries: the last is the total).
     DeviceBuffer cnt, off;
@@ -138,7 +159,8 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
     if (nvec > 0)
         vector_entries<false><<<grid_for(nvec), kThreads, 0, st>>>(
             p->block_offsets.get<int32_t>(), ncells, W, p->atox.get<int32_t>(), p->vals.get<uint16_t>(),
-            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, cnt.get<int32_t>(), nullptr, nullptr, nullptr);
+            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, parts, M, cnt.get<int32_t>(), nullptr, nullptr,
+            nullptr);
     RA_LAUNCH_CHECK("vector_entries count");
     size_t tb = 0;
     RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, tb, cnt.get<int32_t>(), off.get<int32_t>(),
@@ -159,17 +181,15 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
     RA_TRY(v1.allocate(std::max<int64_t>(n, 1) * sizeof(float)));
     RA_TRY(p->f32_vals.allocate(std::max<int64_t>(n, 1) * sizeof(float)));
     RA_TRY(p->f32_colind.allocate(std::max<int64_t>(n, 1) * sizeof(int32_t)));
-    RA_TRY(p->f32_rowptr.allocate((static_cast<int64_t>(M) + 1) * sizeof(int32_t)));
+    RA_TRY(p->f32_rowptr.allocate((R + 1) * sizeof(int32_t)));
     int32_t* rowptr = p->f32_rowptr.get<int32_t>();
-    f32_fill_i32<<<grid_for(M + 1), kThreads, 0, st>>>(rowptr, M + 1, 0);
+    f32_fill_i32<<<grid_for(R + 1), kThreads, 0, st>>>(rowptr, R + 1, 0);
     if (n > 0) {
         vector_entries<true><<<grid_for(nvec), kThreads, 0, st>>>(
             p->block_offsets.get<int32_t>(), ncells, W, p->atox.get<int32_t>(), p->vals.get<uint16_t>(),
-            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, nullptr, off.get<int32_t>(),
+            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, parts, M, nullptr, off.get<int32_t>(),
             keys.get<uint64_t>(), v1.get<float>());
         RA_LAUNCH_CHECK("vector_entries emit");
-        int rbits = 1;
-        while ((int64_t(1) << rbits) < M) ++rbits;
         size_t sb = 0;
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sb, keys.get<uint64_t>(), keys2.get<uint64_t>(),
                                                       v1.get<float>(), p->f32_vals.get<float>(),
@@ -181,26 +201,28 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
         // last[row] = end of the row's entries; a max-scan into rowptr[1..M]
         // fills the rows without entries.
         DeviceBuffer last;
-        RA_TRY(last.allocate(static_cast<size_t>(M) * sizeof(int32_t)));
-        f32_fill_i32<<<grid_for(M), kThreads, 0, st>>>(last.get<int32_t>(), M, 0);
+        RA_TRY(last.allocate(static_cast<size_t>(R) * sizeof(int32_t)));
+        f32_fill_i32<<<grid_for(R), kThreads, 0, st>>>(last.get<int32_t>(), R, 0);
         row_ends<<<grid_for(n), kThreads, 0, st>>>(keys2.get<uint64_t>(), n, last.get<int32_t>(),
                                                    p->f32_colind.get<int32_t>());
         RA_LAUNCH_CHECK("row_ends");
         size_t ms = 0;
         RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, ms, last.get<int32_t>(), rowptr + 1, hipcub::Max(),
-                                                     M, st));
+                                                     static_cast<int>(R), st));
         RA_TRY(tmp.ensure(std::max<size_t>(ms, 1)));
         RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(tmp.get(), ms, last.get<int32_t>(), rowptr + 1, hipcub::Max(),
-                                                     M, st));
+                                                     static_cast<int>(R), st));
         RA_HIP_TRY(hipStreamSynchronize(st));  // before `last`, `keys*`, `v1` and `tmp` are freed
     }
     p->f32_nnz = n;
+    p->f32_parts = parts;
 
-    // Skewed rows: a ZERO_OVERHEAD_CSR plan over the derived rowptr.
-    ra_features f{};
-    RA_TRY(ra_features_device(rowptr, M, I.K, 16, reinterpret_cast<ra_stream_t>(st), &f));
-    if (f.degree_cv >= kF32RouteZoCv) {
-        RA_TRY(ra_zo_plan_create_device(rowptr, M, I.K, reinterpret_cast<ra_stream_t>(st), &p->f32_zo));
+    // Skewed rows (one column range): a ZERO_OVERHEAD_CSR plan over the derived rowptr.
+    if (parts == 1) {
+        ra_features f{};
+        RA_TRY(ra_features_device(rowptr, M, I.K, 16, reinterpret_cast<ra_stream_t>(st), &f));
+        if (f.degree_cv >= kF32RouteZoCv)
+            RA_TRY(ra_zo_plan_create_device(rowptr, M, I.K, reinterpret_cast<ra_stream_t>(st), &p->f32_zo));
     }
     RA_HIP_TRY(hipStreamSynchronize(st));
     p->f32_ready = true;
@@ -213,8 +235,13 @@ ra_status tile_f32_run(ra_tile_plan* p, const float* B, float* C, int32_t N, hip
     if (p->f32_zo)
         return ra_zo_plan_run(p->f32_zo, p->f32_rowptr.get<int32_t>(), p->f32_colind.get<int32_t>(),
                               p->f32_vals.get<float>(), B, C, N, s);
-    return ra_spmm_csr_direct(p->f32_rowptr.get<int32_t>(), p->f32_colind.get<int32_t>(), p->f32_vals.get<float>(),
-                              B, C, p->info.M, p->info.K, N, p->f32_nnz, s);
+    // Column ranges in ascending order; each continues the fma chains the
+    // previous one stored in C, so the result is the single chain per element.
+    const int64_t M = p->info.M;
+    for (int q = 0; q < p->f32_parts; ++q)
+        RA_TRY(csr_direct_launch(p->f32_rowptr.get<int32_t>() + q * M, p->f32_colind.get<int32_t>(),
+                                 p->f32_vals.get<float>(), B, C, p->info.M, p->info.K, N, p->f32_nnz, q > 0, st));
+    return RA_OK;
 }
 
 }  // namespace ra

@@ -75,6 +75,7 @@ struct ra_tile_plan {
     // ZERO_OVERHEAD_CSR plan over it when the row lengths are skewed.
     bool f32_ready = false;
     int64_t f32_nnz = 0;
+    int32_t f32_parts = 1;  // column ranges of the derived CSR (rowptr holds parts * M + 1)
     ra::DeviceBuffer f32_rowptr, f32_colind, f32_vals;
     ra_zo_plan* f32_zo = nullptr;
     ra_tile_plan() = default;
