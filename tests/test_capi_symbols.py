@@ -58,8 +58,8 @@ def test_invalid_arguments_return_status_not_crash():
 
 
 def test_header_is_plain_c(tmp_path):
-    """The boundary header compiles as ISO C99 (no C++ in the signatures), so a
-    C, cgo or FFI host can include it."""
+    """The boundary header compiles as ISO C99 on its own (no C++ and no HIP
+    header in the signatures), so a C, cgo or FFI host can include it."""
     import shutil
     import subprocess
     gcc = shutil.which("gcc")
@@ -69,6 +69,6 @@ def test_header_is_plain_c(tmp_path):
     src.write_text('#include "ra_spmm.h"\nint main(void) { ra_tile_info i; ra_features f; (void)i; (void)f; '
                    'return ra_abi_version() == 1 ? 0 : 1; }\n')
     proc = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-fsyntax-only",
-                           "-I", str(HEADER.parent), "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", str(src)],
+                           "-I", str(HEADER.parent), str(src)],
                           capture_output=True, text=True)
     assert proc.returncode == 0, proc.stderr
