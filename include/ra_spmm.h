@@ -205,6 +205,15 @@ ra_status ra_spmm_csr_baseline(const int32_t* d_rowptr, const int32_t* d_colind,
                                const float* d_vals, const float* d_B, float* d_C,
                                int32_t M, int32_t K, int32_t N, int64_t nnz,
                                ra_stream_t stream);
+/* Precision-matched baseline: the same kernel with A values and B stored as
+ * IEEE fp16 bits (d_vals_h [nnz], d_B_h [K,N]) and fp32 products and sums into
+ * fp32 C.  Replaces the fp16 cuSPARSE guardrail (CuSparseSpMMState with
+ * fp16 = true): spmm_cusparse_fp16_fn / benchmark_cusparse_fp16[_cold]_fn,
+ * bindings/ra_bindings.cpp:895-960. */
+ra_status ra_spmm_csr_baseline_f16(const int32_t* d_rowptr, const int32_t* d_colind,
+                                   const uint16_t* d_vals_h, const uint16_t* d_B_h, float* d_C,
+                                   int32_t M, int32_t K, int32_t N, int64_t nnz,
+                                   ra_stream_t stream);
 
 /* ZERO_OVERHEAD_CSR: O(M) degree binning, small-row lane groups, 256-nnz hub
  * chunks with a deterministic merge.

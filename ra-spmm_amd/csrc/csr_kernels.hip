@@ -165,9 +165,12 @@ __global__ __launch_bounds__(kBlock) void csr_rows_kernel(
 
 // ----------------------------------------------------------------- baseline
 // One wave per row; lane covers columns lane + 64*i (i < 4) of a 256-column tile.
+// T = float, or _Float16 for the precision-matched variant (A and B stored in
+// fp16, products and sums in fp32).
+template <typename T>
 __global__ __launch_bounds__(kBlock) void csr_baseline_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
-    const float* __restrict__ vals, const float* __restrict__ B, float* __restrict__ C,
+    const T* __restrict__ vals, const T* __restrict__ B, float* __restrict__ C,
     int M, int N) {
     const int lane = threadIdx.x & (kWave - 1);
     const int row = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
@@ -177,12 +180,12 @@ __global__ __launch_bounds__(kBlock) void csr_baseline_kernel(
     const int p1 = rowptr[row + 1];
     for (int p = rowptr[row]; p < p1; ++p) {
         const int c = colind[p];
-        const float v = vals[p];
-        const float* b = B + (int64_t)c * N;
+        const float v = static_cast<float>(vals[p]);
+        const T* b = B + (int64_t)c * N;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int n = n0 + 64 * i;
-            if (n < N) acc[i] = __builtin_fmaf(v, b[n], acc[i]);
+            if (n < N) acc[i] = __builtin_fmaf(v, static_cast<float>(b[n]), acc[i]);
         }
     }
 #pragma unroll
@@ -547,8 +550,22 @@ ra_status ra_spmm_csr_baseline(const int32_t* d_rowptr, const int32_t* d_colind,
     if (M == 0 || N == 0) return RA_OK;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     dim3 grid((M + kWavesPerBlock - 1) / kWavesPerBlock, (N + 255) / 256);
-    csr_baseline_kernel<<<grid, kBlock, 0, st>>>(d_rowptr, d_colind, d_vals, d_B, d_C, M, N);
+    csr_baseline_kernel<float><<<grid, kBlock, 0, st>>>(d_rowptr, d_colind, d_vals, d_B, d_C, M, N);
     RA_LAUNCH_CHECK("csr_baseline_kernel");
+    return RA_OK;
+}
+
+ra_status ra_spmm_csr_baseline_f16(const int32_t* d_rowptr, const int32_t* d_colind,
+                                   const uint16_t* d_vals_h, const uint16_t* d_B_h, float* d_C, int32_t M,
+                                   int32_t K, int32_t N, int64_t nnz, ra_stream_t stream) {
+    RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals_h, d_B_h, d_C, M, K, N, nnz));
+    if (M == 0 || N == 0) return RA_OK;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    dim3 grid((M + kWavesPerBlock - 1) / kWavesPerBlock, (N + 255) / 256);
+    csr_baseline_kernel<_Float16><<<grid, kBlock, 0, st>>>(d_rowptr, d_colind,
+                                                           reinterpret_cast<const _Float16*>(d_vals_h),
+                                                           reinterpret_cast<const _Float16*>(d_B_h), d_C, M, N);
+    RA_LAUNCH_CHECK("csr_baseline_kernel_f16");
     return RA_OK;
 }
 

@@ -93,6 +93,33 @@ torch::Tensor spmm_csr_baseline(torch::Tensor rowptr, torch::Tensor colind, torc
     return C;
 }
 
+// Precision-matched baseline on fp16 A values and fp16 B (already converted by
+// the caller; spmm_cusparse_fp16 in ra_spmm/dispatch.py converts first).
+torch::Tensor spmm_csr_baseline_f16(torch::Tensor rowptr, torch::Tensor colind, torch::Tensor vals_h,
+                                    torch::Tensor B_h) {
+    check_gpu_tensor(rowptr, "rowptr");
+    check_gpu_tensor(colind, "colind");
+    check_gpu_tensor(vals_h, "vals");
+    check_gpu_tensor(B_h, "B");
+    TORCH_CHECK(rowptr.scalar_type() == torch::kInt32 && colind.scalar_type() == torch::kInt32,
+                "rowptr/colind must be int32");
+    TORCH_CHECK(vals_h.scalar_type() == torch::kFloat16 && B_h.scalar_type() == torch::kFloat16,
+                "vals and B must be float16");
+    TORCH_CHECK(rowptr.dim() == 1 && rowptr.numel() >= 1 && B_h.dim() == 2, "bad shapes");
+    check_same_device(rowptr, B_h);
+    const c10::DeviceGuard guard(B_h.device());
+    const int M = static_cast<int>(rowptr.size(0)) - 1;
+    const int K = static_cast<int>(B_h.size(0));
+    const int N = static_cast<int>(B_h.size(1));
+    auto C = torch::empty({M, N}, B_h.options().dtype(torch::kFloat32));
+    check(ra_spmm_csr_baseline_f16(rowptr.data_ptr<int32_t>(), colind.data_ptr<int32_t>(),
+                                   static_cast<const uint16_t*>(vals_h.data_ptr()),
+                                   static_cast<const uint16_t*>(B_h.data_ptr()), C.data_ptr<float>(), M, K, N,
+                                   colind.numel(), current_stream()),
+          "spmm_csr_baseline_f16");
+    return C;
+}
+
 // Reusable guardrail plan: keeps the CSR tensors and owns its output, like the
 // reference CuSparsePlanWrapper (bindings/ra_bindings.cpp:620-631, 1025-1037):
 // run_cusparse_plan writes into and returns the same C every call.
@@ -529,6 +556,9 @@ PYBIND11_MODULE(_C, m) {
           pybind11::arg("colind"), pybind11::arg("vals"), pybind11::arg("B"));
 
     // Guardrail names of the reference, served by the baseline CSR kernel.
+    m.def("spmm_csr_baseline_f16", &spmm_csr_baseline_f16,
+          "Precision-matched baseline CSR kernel: fp16 vals and B (float16 tensors), fp32 accumulate and C",
+          pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"), pybind11::arg("B"));
     m.def("spmm_cusparse", &spmm_csr_baseline,
           "Guardrail SpMM (served by the hand-written baseline CSR kernel)",
           pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"),

@@ -24,13 +24,15 @@ from ._C import (  # noqa: F401
     route_features, run_community_tc_plan, run_community_tc_plan_tf32, run_cusparse_plan,
     run_segment_hybrid_plan, run_segment_hybrid_plan_tf32, run_tc_direct_plan,
     run_tc_direct_plan_tf32, run_tile_plan_route, run_zero_overhead_plan, spmm_csr_baseline,
-    spmm_csr_direct, spmm_cusparse,
+    spmm_csr_baseline_f16, spmm_csr_direct, spmm_cusparse,
 )
 from .dispatch import (  # noqa: F401
-    DEPLOYED_KERNELS, TILE_KERNELS, benchmark_cusparse, benchmark_cusparse_cold,
-    build_kernel_plan, gpu_info_next, make_timing_breakdown, measure_exec_ms, measure_one_ms,
-    run_oracle_cold, run_oracle_warm, run_planned_kernel, run_router_cold, run_router_plan,
-    run_router_warm, smallest_strict_crossover,
+    BASE_ATOL, COLD_ITERS, DEPLOYED_KERNELS, HARD_FAIL_THRESHOLD, TC_EXTRA_FACTOR, TILE_KERNELS, TIMED_ITERS,
+    WARMUP, benchmark_cusparse, benchmark_cusparse_cold, benchmark_cusparse_fp16, benchmark_cusparse_fp16_cold,
+    benchmark_custom_cold, build_kernel_plan, correctness_gate, gpu_info_next, make_timing_breakdown,
+    measure_exec_ms, measure_ms, measure_one_ms, population_cv, run_kernel, run_oracle_cold, run_oracle_warm,
+    run_planned_kernel, run_router_cold, run_router_plan, run_router_warm, smallest_strict_crossover,
+    spmm_cusparse_fp16,
 )
 from .router import (  # noqa: F401
     MI355X, REFERENCE, RouterTable, features_from_moments, production_features, route_label,

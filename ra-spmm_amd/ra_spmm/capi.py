@@ -22,7 +22,7 @@ EXPORTED = [
     "ra_abi_version", "ra_status_string", "ra_last_error", "ra_path_name", "ra_reject_name",
     "ra_features_host", "ra_features_device", "ra_features_from_moments", "ra_route_dispatch",
     "ra_analyze_matrix",
-    "ra_spmm_csr_direct", "ra_spmm_csr_baseline", "ra_zo_bins_host", "ra_zo_plan_create",
+    "ra_spmm_csr_direct", "ra_spmm_csr_baseline", "ra_spmm_csr_baseline_f16", "ra_zo_bins_host", "ra_zo_plan_create",
     "ra_zo_plan_create_device", "ra_zo_plan_export", "ra_zo_plan_run", "ra_zo_plan_run_stage", "ra_zo_plan_get_info", "ra_zo_plan_destroy", "ra_tile_host_build",
     "ra_tile_host_get_info", "ra_tile_host_export", "ra_tile_host_destroy",
     "ra_tile_plan_create", "ra_tile_plan_create_device", "ra_tile_plan_export",
@@ -138,6 +138,7 @@ def load():
                                              ctypes.POINTER(Route)]),
         "ra_spmm_csr_direct": (ctypes.c_int, [P, P, P, P, P, I32, I32, I32, I64, P]),
         "ra_spmm_csr_baseline": (ctypes.c_int, [P, P, P, P, P, I32, I32, I32, I64, P]),
+        "ra_spmm_csr_baseline_f16": (ctypes.c_int, [P, P, P, P, P, I32, I32, I32, I64, P]),
         "ra_zo_bins_host": (ctypes.c_int, [P, I32, I32, P, P, P, P, ctypes.POINTER(ZOInfo)]),
         "ra_zo_plan_create": (ctypes.c_int, [P, I32, I32, ctypes.POINTER(P)]),
         "ra_zo_plan_create_device": (ctypes.c_int, [P, I32, I32, P, ctypes.POINTER(P)]),

@@ -1,8 +1,10 @@
 """Label -> plan/run dispatch, timing drivers and one-shot helpers.
 
-Reference: build_kernel_plan / run_planned_kernel / benchmark_custom_cold,
-ra_real_graph_eval.py:247-343; make_timing_breakdown / measure_cuda_exec_ms,
-bench/benchmark.cpp:19-67; benchmark_cusparse[_cold], run_router_plan,
+Reference: build_kernel_plan / run_planned_kernel / run_kernel /
+benchmark_custom_cold, measure_ms, population_cv and the correctness gate,
+ra_real_graph_eval.py:37-51, 210-343, 478-495; make_timing_breakdown / measure_cuda_exec_ms,
+bench/benchmark.cpp:19-67; benchmark_cusparse[_cold], spmm_cusparse_fp16 /
+benchmark_cusparse_fp16[_cold] (bindings/ra_bindings.cpp:895-960), run_router_plan,
 run_router_{warm,cold}, run_oracle_{warm,cold}, bindings/ra_bindings.cpp:821-1037,
 1320-1965.  Timing uses HIP events on the current stream, which is the stream
 every ra_spmm launch goes to.
@@ -59,6 +61,85 @@ def run_planned_kernel(kernel_name, plan, rowptr, colind, vals, B):
     if kernel_name == "SEGMENT_HYBRID_TF32":
         return _C.run_segment_hybrid_plan_tf32(plan, colind, vals, B)
     raise ValueError(f"Unknown planned kernel: {kernel_name}")
+
+
+def run_kernel(kernel_name, rowptr, colind, vals, B, plan_cache: dict, cache_key):
+    """Plan once per cache_key, then run (ra_real_graph_eval.py:288-301).  The
+    guardrail name uses the reusable baseline plan, which owns its C."""
+    if kernel_name == "CUSPARSE":
+        if cache_key not in plan_cache:
+            plan_cache[cache_key] = _C.make_cusparse_plan(rowptr, colind, vals, B)
+        return _C.run_cusparse_plan(plan_cache[cache_key], B)
+    if cache_key not in plan_cache:
+        M = int(rowptr.shape[0]) - 1
+        plan_cache[cache_key] = build_kernel_plan(kernel_name, rowptr.cpu(), colind.cpu(), vals.cpu(), M,
+                                                  int(B.shape[0]), int(B.shape[1]))
+    return run_planned_kernel(kernel_name, plan_cache[cache_key], rowptr, colind, vals, B)
+
+
+# Harness protocol and correctness gate (ra_real_graph_eval.py:37-51).
+WARMUP = 50
+TIMED_ITERS = 200
+COLD_ITERS = 10
+BASE_ATOL = 1e-3
+TC_EXTRA_FACTOR = 10.0
+HARD_FAIL_THRESHOLD = 1.0
+
+
+def population_cv(degrees) -> float:
+    """std (population) / mean of row lengths, 0 for an empty or all-zero
+    vector (ra_real_graph_eval.py:235-242)."""
+    d = torch.as_tensor(degrees).float()
+    if d.numel() == 0:
+        return 0.0
+    mean = d.mean()
+    if float(mean.item()) == 0.0:
+        return 0.0
+    return float((d.std(correction=0) / mean).item())
+
+
+def correctness_gate(kernel_name: str, max_error: float, max_row_nnz: int) -> dict:
+    """The harness's verdict on one kernel's max |C - C_ref|: tolerance
+    1e-3 * sqrt(max row nnz), x10 for the tile paths; errors >= 1 are hard
+    failures (ra_real_graph_eval.py:481-489)."""
+    import math
+    tol = BASE_ATOL * max(1.0, math.sqrt(max(1, int(max_row_nnz))))
+    if kernel_name in TILE_KERNELS:
+        tol *= TC_EXTRA_FACTOR
+    return {"correct": max_error <= tol and max_error < HARD_FAIL_THRESHOLD,
+            "soft_fail": tol < max_error < HARD_FAIL_THRESHOLD,
+            "hard_fail": max_error >= HARD_FAIL_THRESHOLD,
+            "max_error": max_error, "tolerance": tol, "error": ""}
+
+
+def measure_ms(run_fn, warmup: int = WARMUP, iters: int = TIMED_ITERS) -> float:
+    """Warm protocol of the harness: 50 warmup calls, one event pair over 200
+    (ra_real_graph_eval.py:210-221)."""
+    return measure_exec_ms(run_fn, warmup, iters)
+
+
+def benchmark_custom_cold(kernel_name, rowptr_cpu, colind_cpu, vals_cpu, rowptr, colind, vals, B,
+                          iters: int = COLD_ITERS) -> dict:
+    """Cold protocol: plan build (host-timed, synchronised) + one event-timed
+    execution, averaged over `iters`; CSR_DIRECT has no plan
+    (ra_real_graph_eval.py:304-343)."""
+    M = int(rowptr_cpu.numel() - 1)
+    K, N = int(B.shape[0]), int(B.shape[1])
+    n = max(1, iters)
+    plan_total = exec_total = 0.0
+    for _ in range(n):
+        plan = None
+        if kernel_name != "CSR_DIRECT":
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            plan = build_kernel_plan(kernel_name, rowptr_cpu, colind_cpu, vals_cpu, M, K, N)
+            torch.cuda.synchronize()
+            plan_total += (time.perf_counter() - t0) * 1e3
+        out, ms = measure_one_ms(lambda: run_planned_kernel(kernel_name, plan, rowptr, colind, vals, B))
+        exec_total += ms
+        del out, plan
+    pre, cold = plan_total / n, exec_total / n
+    return {"preprocess_ms": pre, "cold_exec_ms": cold, "ms_cold": pre + cold}
 
 
 def smallest_strict_crossover(setup_a: float, exec_a: float, setup_b: float, exec_b: float):
@@ -136,6 +217,42 @@ def benchmark_cusparse_cold(rowptr, colind, vals, B, iters: int = 10) -> dict:
     d = make_timing_breakdown(plan_sum / n, exec_sum / n, int(colind.numel()), int(B.shape[1]))
     d.update(path="CUSPARSE", in_main_portfolio=True, legacy_baseline=False,
              external_baseline=False, cusparse_algorithm=name, preprocess_ms=plan_sum / n)
+    return d
+
+
+def spmm_cusparse_fp16(rowptr, colind, vals, B):
+    """Precision-matched guardrail, one shot: A values and B rounded to fp16,
+    products and sums in fp32, C fp32 (bindings/ra_bindings.cpp:895-907)."""
+    return _C.spmm_csr_baseline_f16(rowptr, colind, vals.contiguous().half(), B.contiguous().half())
+
+
+def benchmark_cusparse_fp16(rowptr, colind, vals, B, warmup: int = 3, iters: int = 10) -> dict:
+    """Warm precision-matched guardrail timing: conversion outside the timed
+    loop, as the reference's state build (bindings/ra_bindings.cpp:909-932)."""
+    vh, bh = vals.contiguous().half(), B.contiguous().half()
+    ms = measure_exec_ms(lambda: _C.spmm_csr_baseline_f16(rowptr, colind, vh, bh), warmup, max(1, iters))
+    d = make_timing_breakdown(0.0, ms, int(colind.numel()), int(B.shape[1]))
+    d.update(path="CUSPARSE_FP16", in_main_portfolio=False, legacy_baseline=False, external_baseline=True,
+             cusparse_algorithm="csr_baseline_kernel_f16", preprocess_ms=0.0)
+    return d
+
+
+def benchmark_cusparse_fp16_cold(rowptr, colind, vals, B, iters: int = 10) -> dict:
+    """Cold precision-matched guardrail timing: fp16 conversion of A values and
+    B (the state build) plus one execution, averaged (bindings/ra_bindings.cpp:935-960)."""
+    plan_sum = exec_sum = 0.0
+    for _ in range(max(1, iters)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        vh, bh = vals.contiguous().half(), B.contiguous().half()
+        torch.cuda.synchronize()
+        plan_sum += (time.perf_counter() - t0) * 1e3
+        _, ms = measure_one_ms(lambda: _C.spmm_csr_baseline_f16(rowptr, colind, vh, bh))
+        exec_sum += ms
+    n = float(max(1, iters))
+    d = make_timing_breakdown(plan_sum / n, exec_sum / n, int(colind.numel()), int(B.shape[1]))
+    d.update(path="CUSPARSE_FP16", in_main_portfolio=False, legacy_baseline=False, external_baseline=True,
+             cusparse_algorithm="csr_baseline_kernel_f16", preprocess_ms=plan_sum / n)
     return d
 
 

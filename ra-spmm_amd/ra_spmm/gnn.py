@@ -29,11 +29,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _C
-from .dispatch import TILE_KERNELS, build_kernel_plan, run_planned_kernel
+from .dispatch import BASE_ATOL, TC_EXTRA_FACTOR, TILE_KERNELS, build_kernel_plan, run_planned_kernel
 from .router import route_label
 
-BASE_ATOL = 1e-3        # ra_real_graph_eval.py:41-51
-TC_EXTRA_FACTOR = 10.0
 
 _FIXED = {"csr_direct": "CSR_DIRECT", "zero_overhead": "ZERO_OVERHEAD_CSR",
           "tc_direct": "TC_DIRECT", "tc_direct_tf32": "TC_DIRECT_TF32",

@@ -244,3 +244,45 @@ def test_c5_full_size_routed_widths(oracle):
         np.testing.assert_array_equal(C[short], seq[short])
         assert_close_scaled(C, oracle.spmm_f64(sub_rp, sub_ci, sub_vl, Bn),
                             oracle.spmm_f64(sub_rp, sub_ci, np.abs(sub_vl), np.abs(Bn)), 1e-5, f"C5 N={N}")
+
+
+def test_precision_matched_guardrail_fp16(oracle):
+    """spmm_cusparse_fp16 (bindings/ra_bindings.cpp:895-907): A values and B
+    rounded to fp16, one fp32 fma chain per element in CSR order: bit-identical
+    to the oracle's chain on the rounded inputs.  Its warm/cold timing dicts
+    carry the reference's keys."""
+    g = S.random_csr(1500, 1200, 14.0, seed=21, skew=1.1, empty_frac=0.03)
+    rp, ci, vl = _dev(g)
+    for N in (1, 47, 64, 300):
+        B = _B(g.K, N, seed=N)
+        C = ra_spmm.spmm_cusparse_fp16(rp, ci, vl, torch.from_numpy(B).cuda()).cpu().numpy()
+        ref = oracle.spmm_seq_f32(g.rowptr, g.colind, oracle.quantize_f16(g.vals), oracle.quantize_f16(B))
+        np.testing.assert_array_equal(C, ref, err_msg=f"N={N}")
+    Bd = torch.from_numpy(_B(g.K, 64, seed=1)).cuda()
+    warm = ra_spmm.benchmark_cusparse_fp16(rp, ci, vl, Bd, warmup=1, iters=3)
+    cold = ra_spmm.benchmark_cusparse_fp16_cold(rp, ci, vl, Bd, iters=2)
+    for d in (warm, cold):
+        assert d["path"] == "CUSPARSE_FP16" and d["exec_ms"] > 0 and d["external_baseline"]
+        assert {"plan_ms", "exec_ms", "total_ms", "gflops", "preprocess_ms", "cusparse_algorithm"} <= set(d)
+    assert cold["plan_ms"] > 0
+
+
+def test_harness_helpers_run_every_deployed_kernel(oracle):
+    """run_kernel / benchmark_custom_cold / correctness_gate as the real-graph
+    harness uses them (ra_real_graph_eval.py:288-343, 478-495)."""
+    g = S.random_csr(900, 900, 10.0, seed=4, skew=1.0)
+    rp, ci, vl = _dev(g)
+    B = torch.from_numpy(_B(g.K, 32, seed=2)).cuda()
+    C_ref = ra_spmm.spmm_cusparse(rp, ci, vl, B)
+    max_row = int(np.diff(g.rowptr).max())
+    cache = {}
+    for k in ra_spmm.DEPLOYED_KERNELS + ["CUSPARSE"]:
+        out = ra_spmm.run_kernel(k, rp, ci, vl, B, cache, (k, 32))
+        gate = ra_spmm.correctness_gate(k, float((out - C_ref).abs().max()), max_row)
+        assert gate["correct"], (k, gate)
+        cold = ra_spmm.benchmark_custom_cold(k, rp.cpu(), ci.cpu(), vl.cpu(), rp, ci, vl, B, 2) \
+            if k != "CUSPARSE" else None
+        if cold:
+            assert cold["cold_exec_ms"] > 0 and (cold["preprocess_ms"] > 0) == (k != "CSR_DIRECT")
+    assert len(cache) == len(ra_spmm.DEPLOYED_KERNELS) + 1
+    assert ra_spmm.measure_ms(lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B), 2, 5) > 0

@@ -22,6 +22,17 @@ REQUIRED = {
     "run_segment_hybrid_plan_tf32": ["plan", "colind", "vals", "B"],
     "spmm_cusparse": ["rowptr", "colind", "vals", "B"],
     "analyze_matrix": ["rowptr", "colind", "M", "K", "N"],
+    "spmm_cusparse_fp16": ["rowptr", "colind", "vals", "B"],
+    "benchmark_cusparse_fp16": ["rowptr", "colind", "vals", "B", "warmup", "iters"],
+    "benchmark_cusparse_fp16_cold": ["rowptr", "colind", "vals", "B", "iters"],
+    # harness helpers of ra_real_graph_eval.py (the a17 call site)
+    "build_kernel_plan": ["kernel_name", "rowptr_cpu", "colind_cpu", "vals_cpu", "M", "K", "N"],
+    "run_planned_kernel": ["kernel_name", "plan", "rowptr", "colind", "vals", "B"],
+    "run_kernel": ["kernel_name", "rowptr", "colind", "vals", "B", "plan_cache", "cache_key"],
+    "benchmark_custom_cold": ["kernel_name", "rowptr_cpu", "colind_cpu", "vals_cpu", "rowptr", "colind", "vals",
+                              "B", "iters"],
+    "measure_ms": ["run_fn", "warmup", "iters"],
+    "population_cv": ["degrees"],
 }
 OPTIONAL = ["make_cusparse_plan", "run_cusparse_plan", "benchmark_cusparse", "benchmark_cusparse_cold",
             "run_router_plan", "run_router_warm", "run_router_cold", "run_oracle_warm", "run_oracle_cold",
@@ -55,3 +66,23 @@ def test_optional_names_and_plan_classes():
             assert hasattr(getattr(ra_spmm, cls), prop), (cls, prop)
     for prop in ("valid", "M", "K", "plan_bytes", "num_tiny", "num_long"):
         assert hasattr(ra_spmm.RAZeroOverheadPlan, prop), prop
+
+
+def test_correctness_gate_and_cv_follow_the_harness():
+    """ra_real_graph_eval.py:37-51, 235-242, 481-489: tolerance 1e-3 sqrt(max row
+    nnz), x10 for tile paths, hard failure at 1.0; population CV."""
+    import math
+    import torch
+    assert (ra_spmm.WARMUP, ra_spmm.TIMED_ITERS, ra_spmm.COLD_ITERS) == (50, 200, 10)
+    g = ra_spmm.correctness_gate("CSR_DIRECT", 0.0099, 100)
+    assert g["correct"] and math.isclose(g["tolerance"], 0.01)
+    g = ra_spmm.correctness_gate("COMMUNITY_TC_TF32", 0.05, 100)
+    assert g["correct"] and math.isclose(g["tolerance"], 0.1)
+    g = ra_spmm.correctness_gate("ZERO_OVERHEAD_CSR", 0.5, 0)   # max row clamps to 1: tol 1e-3
+    assert g["soft_fail"] and not g["correct"] and not g["hard_fail"]
+    g = ra_spmm.correctness_gate("TC_DIRECT", 1.0, 10**8)        # tol 100, but >= 1.0 is hard
+    assert g["hard_fail"] and not g["correct"] and not g["soft_fail"]
+    assert ra_spmm.population_cv(torch.tensor([2, 2, 2])) == 0.0
+    assert ra_spmm.population_cv(torch.tensor([0, 0])) == 0.0
+    assert ra_spmm.population_cv(torch.tensor([], dtype=torch.int32)) == 0.0
+    assert math.isclose(ra_spmm.population_cv(torch.tensor([1, 3])), 0.5, rel_tol=1e-6)
