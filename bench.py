@@ -390,6 +390,7 @@ def main(argv=None):
                        force_path=args.path)
     achieved = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9
     copy_gbs = hbm_copy_gbs()
+    traffic = args.traffic if args.traffic is not None else profile_traffic(res["kernel"], args.config, res["N"])
     line = {
         "metric": METRIC, "value": round(res["gflops"], 3), "unit": "GFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
@@ -400,9 +401,13 @@ def main(argv=None):
                    "N": res["N"], "router_table": args.table},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": args.traffic if args.traffic is not None else
-                     profile_traffic(res["kernel"], args.config, res["N"]), "kernel": res["kernel"],
+                     "traffic": traffic, "kernel": res["kernel"],
                      "kernel_ms": round(res["kernel_ms"], 5), "bytes_alg": res["bytes_alg"],
+                     # HBM bytes the kernel actually moves (rocprofv3 FETCH + WRITE per
+                     # launch) over this run's launch time, against the same peak.
+                     "traffic_gbs": round(traffic / (res["kernel_ms"] * 1e-3) / 1e9, 1) if traffic else None,
+                     "traffic_frac": round(traffic / (res["kernel_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+                     if traffic else None,
                      "measured_copy_gbs": round(copy_gbs, 1)},
         "cpu_baseline": res.get("cpu_port"),
         "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
