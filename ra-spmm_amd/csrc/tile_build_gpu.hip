@@ -3,9 +3,10 @@
 // Same windows, vectors, blocks, value rounding and segment tables as the host
 // builder (tile_build.cpp), produced with sorts and scans on the GPU:
 //   1. (COMMUNITY_TC) rows sorted by (leading column or INT_MAX, row) -> window slots
-//   2. one 64-bit key per nonzero: (window << 34) | (column << 3) | slot
-//   3. stable radix sort of (key, CSR position)  -> per-window (col, slot) order,
-//      duplicates adjacent in CSR order
+//   2. the row of every nonzero (row starts marked, then a max-scan) and one
+//      64-bit key per nonzero: (cell << (31 + log2 rows)) | (column << log2 rows) | slot
+//   3. stable radix sort of (key, value)  -> per-window (col, slot) order,
+//      duplicates adjacent in CSR order, values in key order
 //   4. scans: vector ids, vectors and blocks per window, block offsets
 //   5. scatter: atox (first entry of each vector), values (first entry of each
 //      (col, slot) sums its duplicates in CSR order, scales, rounds)
@@ -109,27 +110,35 @@ struct Layout {
     int vb;
 };
 
-// Key of every nonzero: (window << (31 + sb)) | (column << sb) | slot; the row
-// of position p is found by binary search.
+// Row of every nonzero position: each non-empty row marks its first position,
+// then an inclusive max-scan carries it over the row (rows ascend with
+// position).  Two streaming passes instead of a binary search per nonzero
+// (18 dependent loads each on C4).
+__global__ void mark_row_starts(const int32_t* __restrict__ rowptr, int M, int64_t base,
+                                int32_t* __restrict__ row_of) {
+    RA_GRID_STRIDE(r, (int64_t)M) {
+        if (rowptr[r + 1] > rowptr[r]) row_of[rowptr[r] - base] = static_cast<int32_t>(r);
+    }
+}
+
+// Key of every nonzero: (window << (31 + sb)) | (column << sb) | slot.
 // With column partitions the "window" of a key is the cell
 // part * W + window, part = column / cols_per_part (partition-major cells).
-__global__ void entry_keys(const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
-                           const int32_t* __restrict__ pos, int M, int64_t base, int64_t n, int sb,
-                           int cols_per_part, int64_t W, uint64_t* __restrict__ keys, int32_t* __restrict__ idx) {
+// vout (when given) receives each nonzero's value, so that the key sort
+// carries the values along and the scatter reads them in key order.
+__global__ void entry_keys(const int32_t* __restrict__ row_of, const int32_t* __restrict__ colind,
+                           const float* __restrict__ vals, const int32_t* __restrict__ pos, int64_t base, int64_t n,
+                           int sb, int cols_per_part, int64_t W, uint64_t* __restrict__ keys,
+                           float* __restrict__ vout) {
     RA_GRID_STRIDE(t, n) {
         const int64_t p = base + t;
-        int lo = 0, hi = M - 1;  // last row with rowptr[row] <= p
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (rowptr[mid] <= p) lo = mid;
-            else hi = mid - 1;
-        }
+        const int lo = row_of[t];
         const int64_t slot_pos = pos ? pos[lo] : lo;
         const int64_t cell = (int64_t)(colind[p] / cols_per_part) * W + (slot_pos >> sb);
         keys[t] = (static_cast<uint64_t>(cell) << (31 + sb)) |
                   (static_cast<uint64_t>(static_cast<uint32_t>(colind[p])) << sb) |
                   static_cast<uint64_t>(slot_pos & ((1 << sb) - 1));
-        if (idx) idx[t] = static_cast<int32_t>(t);
+        if (vout) vout[t] = vals[p];
     }
 }
 
@@ -200,9 +209,8 @@ __global__ void window_counts(const int32_t* __restrict__ nvec, int W, int vb, i
     }
 }
 
-__global__ void scatter_entries(const uint64_t* __restrict__ keys, const int32_t* __restrict__ idx,
-                                const int32_t* __restrict__ vid, const int32_t* __restrict__ newkey,
-                                int64_t n, const float* __restrict__ vals, int64_t base,
+__global__ void scatter_entries(const uint64_t* __restrict__ keys, const float* __restrict__ svals,
+                                const int32_t* __restrict__ vid, const int32_t* __restrict__ newkey, int64_t n,
                                 const int32_t* __restrict__ block_offsets,
                                 const int32_t* __restrict__ win_vec_start, float vscale, int bf16, Layout L,
                                 int32_t* __restrict__ atox, uint16_t* __restrict__ out) {
@@ -218,8 +226,8 @@ __global__ void scatter_entries(const uint64_t* __restrict__ keys, const int32_t
         const int kk = static_cast<int>(vlocal % L.vb);
         atox[blk * L.vb + kk] = col;
         // Duplicates of (window, col, slot) follow in CSR order (stable sort).
-        float acc = 0.f + vals[base + idx[i]];
-        for (int64_t j = i + 1; j < n && keys[j] == k; ++j) acc += vals[base + idx[j]];
+        float acc = 0.f + svals[i];
+        for (int64_t j = i + 1; j < n && keys[j] == k; ++j) acc += svals[j];
         // 8-row blocks: [slot][vector]; tall blocks: [slot/16][vector/8][slot%16][vector%8],
         // the 16-byte run one MFMA lane (row slot%16, K group vector/8) loads.
         const int64_t at = L.vb == 8 ? blk * 64 + slot * 8 + kk
@@ -336,7 +344,8 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     size_t sort_bytes = 0, scan_bytes = 0, red_bytes = 0;
     uint64_t* knull = nullptr;
     int32_t* inull = nullptr;
-    RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, knull, knull, inull, inull,
+    float* fnull = nullptr;
+    RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, knull, knull, fnull, fnull,
                                                   static_cast<int>(std::max<int64_t>(nn, M)), 0, 64, st));
     RA_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, inull, inull, static_cast<int>(nn), st));
     size_t scan2 = 0;
@@ -350,9 +359,13 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     size_t red2 = 0;
     RA_HIP_TRY(hipcub::DeviceReduce::Sum(nullptr, red2, inull, inull, static_cast<int>(nn), st));
     red_bytes = std::max(red_bytes, red2);
+    size_t scan4 = 0;
+    RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, scan4, inull, inull, hipcub::Max(), static_cast<int>(nn),
+                                                 st));
+    scan_bytes = std::max(scan_bytes, scan4);
     const size_t tmp_bytes = std::max({sort_bytes, scan_bytes, red_bytes});
 
-    const size_t need = 256 * 26 + tmp_bytes + nn * (2 * 8 + 2 * 4 + 3 * 4) +
+    const size_t need = 256 * 27 + tmp_bytes + nn * (2 * 8 + 2 * 4 + 4 * 4) +
                         std::max<int64_t>(M, 1) * (2 * 8 + 4 + 4) + (Wmax + 1) * 4 * 9 + 64;
     Scratch s;
     RA_TRY(s.buf.allocate(need));
@@ -360,11 +373,12 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     void* tmp = s.take<char>(tmp_bytes, off);
     uint64_t* keys = s.take<uint64_t>(nn, off);
     uint64_t* keys2 = s.take<uint64_t>(nn, off);
-    int32_t* idx = s.take<int32_t>(nn, off);
-    int32_t* idx2 = s.take<int32_t>(nn, off);
+    float* fval = s.take<float>(nn, off);   // values in CSR order, then sorted with the keys
+    float* fval2 = s.take<float>(nn, off);
     int32_t* newvec = s.take<int32_t>(nn, off);
     int32_t* newkey = s.take<int32_t>(nn, off);
     int32_t* vid = s.take<int32_t>(nn, off);
+    int32_t* row_of = s.take<int32_t>(nn, off);
     uint64_t* rkeys = s.take<uint64_t>(std::max<int64_t>(M, 1), off);
     uint64_t* rkeys2 = s.take<uint64_t>(std::max<int64_t>(M, 1), off);
     int32_t* pos = s.take<int32_t>(std::max<int64_t>(M, 1), off);
@@ -396,6 +410,16 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     p->info.value_scale_log2 = bf16 ? 0 : ra::f16_value_scale_log2(vmax);
     const float vscale = std::ldexp(1.0f, p->info.value_scale_log2);
 
+    // Row of every nonzero (rowptr is monotone by now): marks in `newvec`,
+    // which mark_new overwrites later, max-scanned into row_of.
+    if (n > 0) {
+        fill_i32<<<grid_for(n), kThreads, 0, st>>>(newvec, n, 0);
+        mark_row_starts<<<grid_for(M), kThreads, 0, st>>>(rowptr, M, base, newvec);
+        size_t tb = tmp_bytes;
+        RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(tmp, tb, newvec, row_of, hipcub::Max(), static_cast<int>(n), st));
+        RA_LAUNCH_CHECK("row ids");
+    }
+
     // Row order: COMMUNITY_TC sorts rows by leading column (ties by row).
     const int32_t* pos_ptr = nullptr;
     const int32_t* order_ptr = nullptr;
@@ -421,7 +445,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         rows = ra::kTileWindow;
         if (n > 0) {
             fill_u32<<<1, kThreads, 0, st>>>(reinterpret_cast<unsigned*>(layout_counts), 6);
-            entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, 5, INT32_MAX,
+            entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, 5, INT32_MAX,
                                                          (M + 31) / 32, keys, nullptr);
             int wb = 0;
             while ((int64_t(1) << wb) < (M + 31) / 32) ++wb;
@@ -458,10 +482,10 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     const int wshift = 31 + L.sb;
     if (wshift + wbits > 64) return ra::fail(RA_ERR_UNSUPPORTED, "tile: sort key wider than 64 bits");
     if (n > 0) {
-        entry_keys<<<grid_for(n), kThreads, 0, st>>>(rowptr, colind, pos_ptr, M, base, n, L.sb, cols_per_part, W,
-                                                     keys, idx);
+        entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, L.sb, cols_per_part,
+                                                     W, keys, fval);
         size_t tb = tmp_bytes;
-        RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, keys2, idx, idx2, static_cast<int>(n),
+        RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, keys2, fval, fval2, static_cast<int>(n),
                                                       0, wshift + wbits, st));
         mark_new<<<grid_for(n), kThreads, 0, st>>>(keys2, n, L.sb, newvec, newkey);
         tb = tmp_bytes;
@@ -526,7 +550,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     fill_i32<<<grid_for(nblocks * L.vb), kThreads, 0, st>>>(p->atox.get<int32_t>(), nblocks * L.vb, -1);
     fill_u16<<<grid_for(nblocks * block_vals), kThreads, 0, st>>>(p->vals.get<uint16_t>(), nblocks * block_vals);
     if (n > 0)
-        scatter_entries<<<grid_for(n), kThreads, 0, st>>>(keys2, idx2, vid, newkey, n, vals, base, boff,
+        scatter_entries<<<grid_for(n), kThreads, 0, st>>>(keys2, fval2, vid, newkey, n, boff,
                                                           wvec_start, vscale, bf16 ? 1 : 0, L,
                                                           p->atox.get<int32_t>(), p->vals.get<uint16_t>());
     RA_LAUNCH_CHECK("scatter_entries");
