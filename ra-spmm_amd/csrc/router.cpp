@@ -59,12 +59,13 @@ constexpr RouterTable kReference = {
 // MI355X calibration (structure of the tree unchanged; measured on gfx950 with
 // bench.py --sweep over the five benchmark configs C1-C5):
 //  - tile gate: the device tile build (sorts and scans on the GPU) runs at
-//    1.1-1.8e-10 s per nnz (C2 1.6e7 nnz: 2.8 ms; C4 1.24e8 nnz: 13.5 ms),
+//    1.6-2.3e-10 s per nnz (C2 1.6e7 nnz: 3.6 ms; C4 1.24e8 nnz: 19.5 ms),
 //    plus ~3e-10 s per nnz to upload a host CSR (the host builder took
 //    0.75-1.5e-8 s per nnz), so the estimate is 1e-9 s per nnz with the same
 //    20 s budget;
-//  - FP32-route tile picks go to the CSR family: on the ER graph of config 1
-//    CSR_DIRECT takes 9-14 us against 25-42 us for the FP32 tile route;
+//  - FP32-route tile picks go to the CSR family, which needs no plan: the FP32
+//    tile route runs the same CSR kernels on the plan's stored values, after a
+//    tile build (C1: 3.3 ms) and a one-time derivation of that CSR;
 //  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR:
 //    one lane group per hub row is 6.6x slower on config 2.
 //  - rule 2's remaining uniform graphs at N <= 64 go to CSR_DIRECT: at 64
