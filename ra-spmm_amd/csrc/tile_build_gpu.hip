@@ -4,7 +4,8 @@
 // builder (tile_build.cpp), produced with sorts and scans on the GPU:
 //   1. (COMMUNITY_TC) rows sorted by (leading column or INT_MAX, row) -> window slots
 //   2. the row of every nonzero (row starts marked, then a max-scan) and one
-//      64-bit key per nonzero: (cell << (31 + log2 rows)) | (column << log2 rows) | slot
+//      64-bit key per nonzero: (cell << (cb + log2 rows)) | (column << log2 rows) | slot,
+//      cb = bits of K - 1 (the fewer key bits, the fewer radix passes)
 //   3. stable radix sort of (key, value)  -> per-window (col, slot) order,
 //      duplicates adjacent in CSR order, values in key order
 //   4. scans: vector ids, vectors and blocks per window, block offsets
@@ -108,6 +109,7 @@ __global__ void fill_win_rows(const int32_t* __restrict__ order, int M, int64_t 
 struct Layout {
     int sb;
     int vb;
+    int cb;  // column bits of the sort key
 };
 
 // Row of every nonzero position: each non-empty row marks its first position,
@@ -121,21 +123,21 @@ __global__ void mark_row_starts(const int32_t* __restrict__ rowptr, int M, int64
     }
 }
 
-// Key of every nonzero: (window << (31 + sb)) | (column << sb) | slot.
+// Key of every nonzero: (window << (cb + sb)) | (column << sb) | slot.
 // With column partitions the "window" of a key is the cell
 // part * W + window, part = column / cols_per_part (partition-major cells).
 // vout (when given) receives each nonzero's value, so that the key sort
 // carries the values along and the scatter reads them in key order.
 __global__ void entry_keys(const int32_t* __restrict__ row_of, const int32_t* __restrict__ colind,
                            const float* __restrict__ vals, const int32_t* __restrict__ pos, int64_t base, int64_t n,
-                           int sb, int cols_per_part, int64_t W, uint64_t* __restrict__ keys,
+                           int sb, int cb, int cols_per_part, int64_t W, uint64_t* __restrict__ keys,
                            float* __restrict__ vout) {
     RA_GRID_STRIDE(t, n) {
         const int64_t p = base + t;
         const int lo = row_of[t];
         const int64_t slot_pos = pos ? pos[lo] : lo;
         const int64_t cell = (int64_t)(colind[p] / cols_per_part) * W + (slot_pos >> sb);
-        keys[t] = (static_cast<uint64_t>(cell) << (31 + sb)) |
+        keys[t] = (static_cast<uint64_t>(cell) << (cb + sb)) |
                   (static_cast<uint64_t>(static_cast<uint32_t>(colind[p])) << sb) |
                   static_cast<uint64_t>(slot_pos & ((1 << sb) - 1));
         if (vout) vout[t] = vals[p];
@@ -218,8 +220,8 @@ __global__ void scatter_entries(const uint64_t* __restrict__ keys, const float* 
     RA_GRID_STRIDE(i, n) {
         if (!newkey[i]) continue;
         const uint64_t k = keys[i];
-        const int64_t w = static_cast<int64_t>(k >> (31 + L.sb));
-        const int32_t col = static_cast<int32_t>((k >> L.sb) & 0x7FFFFFFFu);
+        const int64_t w = static_cast<int64_t>(k >> (L.cb + L.sb));
+        const int32_t col = static_cast<int32_t>((k >> L.sb) & ((uint64_t(1) << L.cb) - 1));
         const int slot = static_cast<int>(k & static_cast<uint64_t>(rows - 1));
         const int64_t vlocal = (int64_t)(vid[i] - 1) - win_vec_start[w];
         const int64_t blk = block_offsets[w] + vlocal / L.vb;
@@ -336,6 +338,8 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16) P = v;
     }
     const int cols_per_part = static_cast<int>((static_cast<int64_t>(K) + P - 1) / P);
+    int cb = 1;  // column bits of the sort keys: columns are < K <= 2^cb
+    while ((int64_t(1) << cb) < K) ++cb;
     const int64_t Wmax = (M + ra::kTileWindow - 1) / ra::kTileWindow * P;  // most cells of any layout
     const bool bf16 = value_dtype == RA_DTYPE_BF16;
     const int64_t nn = std::max<int64_t>(n, 1);
@@ -445,12 +449,13 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         rows = ra::kTileWindow;
         if (n > 0) {
             fill_u32<<<1, kThreads, 0, st>>>(reinterpret_cast<unsigned*>(layout_counts), 6);
-            entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, 5, INT32_MAX,
+            entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, 5, cb, INT32_MAX,
                                                          (M + 31) / 32, keys, nullptr);
             int wb = 0;
             while ((int64_t(1) << wb) < (M + 31) / 32) ++wb;
             size_t tb = tmp_bytes;
-            RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, keys, keys2, static_cast<int>(n), 0, 36 + wb, st));
+            RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, keys, keys2, static_cast<int>(n), 0, 5 + cb + wb,
+                                                         st));
             count_layouts<<<std::min<unsigned>(grid_for(n), kReduceBlocks), kThreads, 0, st>>>(keys2, n,
                                                                                                 layout_counts);
             RA_LAUNCH_CHECK("count_layouts");
@@ -461,7 +466,7 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     }
     if (rows != 8 && rows != 16 && rows != 32)
         return ra::fail(RA_ERR_INVALID_ARGUMENT, "tile: rows per window must be 8, 16 or 32");
-    const Layout L{rows == 8 ? 3 : rows == 16 ? 4 : 5, rows == 8 ? 8 : 32};
+    const Layout L{rows == 8 ? 3 : rows == 16 ? 4 : 5, rows == 8 ? 8 : 32, cb};
     const int64_t W = (M + rows - 1) / rows;
     const int64_t slots = W * rows;
     // Split limits in vectors: 64 8-vector blocks for SEGMENT_HYBRID (the
@@ -479,11 +484,11 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
         return ra::fail(RA_ERR_UNSUPPORTED, "tile: too many windows x column partitions for int32 cell ids");
     int wbits = 0;
     while ((int64_t(1) << wbits) < NC) ++wbits;
-    const int wshift = 31 + L.sb;
+    const int wshift = L.cb + L.sb;
     if (wshift + wbits > 64) return ra::fail(RA_ERR_UNSUPPORTED, "tile: sort key wider than 64 bits");
     if (n > 0) {
-        entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, L.sb, cols_per_part,
-                                                     W, keys, fval);
+        entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, L.sb, L.cb,
+                                                     cols_per_part, W, keys, fval);
         size_t tb = tmp_bytes;
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, keys2, fval, fval2, static_cast<int>(n),
                                                       0, wshift + wbits, st));

@@ -9,7 +9,8 @@
 // products in CSR form run on the CSR kernels at the gather rate.  So on the
 // first FP32-route call a plan derives, on the device:
 //   1. per vector, the number of nonzero stored values (count pass, then scan)
-//   2. one key (row << 31 | column) and exact fp32 value per stored nonzero
+//   2. one key (row << cb | column, cb = bits of K - 1) and exact fp32 value
+//      per stored nonzero
 //   3. a radix sort of (key, value): rows ascending, columns ascending within
 //      a row (a plan holds each (row, column) once: duplicates were summed)
 //   4. rowptr from the last index of each row and a max-scan (no atomics)
@@ -75,7 +76,7 @@ template <bool EMIT>
 __global__ void vector_entries(const int32_t* __restrict__ boff, int64_t ncells, int64_t W,
                                const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
                                const int32_t* __restrict__ win_rows, int64_t nvec, int H, int vb, int bf16,
-                               float unscale, int parts, int64_t M, int32_t* __restrict__ count,
+                               float unscale, int parts, int64_t M, int cb, int32_t* __restrict__ count,
                                const int32_t* __restrict__ offset, uint64_t* __restrict__ keys,
                                float* __restrict__ out) {
     RA_GRID_STRIDE(v, nvec) {
@@ -96,7 +97,7 @@ __global__ void vector_entries(const int32_t* __restrict__ boff, int64_t ncells,
                 if ((h & 0x7FFFu) == 0) continue;  // +0 / -0: no product
                 if (EMIT) {
                     const int64_t row = part * M + win_rows[w * H + slot];
-                    keys[o] = (static_cast<uint64_t>(row) << 31) | static_cast<uint32_t>(col);
+                    keys[o] = (static_cast<uint64_t>(row) << cb) | static_cast<uint32_t>(col);
                     out[o] = stored_value(h, bf16 != 0, unscale);
                     ++o;
                 } else {
@@ -110,13 +111,13 @@ __global__ void vector_entries(const int32_t* __restrict__ boff, int64_t ncells,
 
 // last[row] = 1 + index of the row's last entry (rows without entries stay 0;
 // the max-scan then carries the previous row's end).
-__global__ void row_ends(const uint64_t* __restrict__ keys, int64_t n, int32_t* __restrict__ last,
+__global__ void row_ends(const uint64_t* __restrict__ keys, int64_t n, int cb, int32_t* __restrict__ last,
                          int32_t* __restrict__ colind) {
     RA_GRID_STRIDE(i, n) {
         const uint64_t k = keys[i];
-        const int64_t row = static_cast<int64_t>(k >> 31);
-        colind[i] = static_cast<int32_t>(k & 0x7FFFFFFFu);
-        if (i == n - 1 || (keys[i + 1] >> 31) != static_cast<uint64_t>(row)) last[row] = static_cast<int32_t>(i + 1);
+        const int64_t row = static_cast<int64_t>(k >> cb);
+        colind[i] = static_cast<int32_t>(k & ((uint64_t(1) << cb) - 1));
+        if (i == n - 1 || (keys[i + 1] >> cb) != static_cast<uint64_t>(row)) last[row] = static_cast<int32_t>(i + 1);
     }
 }
 
@@ -141,10 +142,12 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
     const int bf16 = I.value_dtype == RA_DTYPE_BF16 ? 1 : 0;
     // Column partitions of the plan are kept (one CSR per column range, run in
     // order) when the (part * M + row, column) key fits 64 bits.
+    int cb = 1;  // columns are < K <= 2^cb
+    while ((int64_t(1) << cb) < I.K) ++cb;
     int parts = std::max(I.col_parts, 1);
     int rbits = 1;
     while ((int64_t(1) << rbits) < (int64_t)parts * M) ++rbits;
-    if (31 + rbits > 64 || (int64_t)parts * M >= INT32_MAX) {
+    if (cb + rbits > 64 || (int64_t)parts * M >= INT32_MAX) {
         parts = 1;
         rbits = 1;
         while ((int64_t(1) << rbits) < M) ++rbits;
@@ -159,8 +162,8 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
     if (nvec > 0)
         vector_entries<false><<<grid_for(nvec), kThreads, 0, st>>>(
             p->block_offsets.get<int32_t>(), ncells, W, p->atox.get<int32_t>(), p->vals.get<uint16_t>(),
-            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, parts, M, cnt.get<int32_t>(), nullptr, nullptr,
-            nullptr);
+            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, parts, M, cb, cnt.get<int32_t>(), nullptr,
+            nullptr, nullptr);
     RA_LAUNCH_CHECK("vector_entries count");
     size_t tb = 0;
     RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, tb, cnt.get<int32_t>(), off.get<int32_t>(),
@@ -187,23 +190,23 @@ ra_status tile_f32_prepare(ra_tile_plan* p, hipStream_t st) {
     if (n > 0) {
         vector_entries<true><<<grid_for(nvec), kThreads, 0, st>>>(
             p->block_offsets.get<int32_t>(), ncells, W, p->atox.get<int32_t>(), p->vals.get<uint16_t>(),
-            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, parts, M, nullptr, off.get<int32_t>(),
+            p->win_rows.get<int32_t>(), nvec, H, vb, bf16, unscale, parts, M, cb, nullptr, off.get<int32_t>(),
             keys.get<uint64_t>(), v1.get<float>());
         RA_LAUNCH_CHECK("vector_entries emit");
         size_t sb = 0;
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sb, keys.get<uint64_t>(), keys2.get<uint64_t>(),
                                                       v1.get<float>(), p->f32_vals.get<float>(),
-                                                      static_cast<int>(n), 0, 31 + rbits, st));
+                                                      static_cast<int>(n), 0, cb + rbits, st));
         RA_TRY(tmp.ensure(std::max<size_t>(sb, 1)));
         RA_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp.get(), sb, keys.get<uint64_t>(), keys2.get<uint64_t>(),
                                                       v1.get<float>(), p->f32_vals.get<float>(),
-                                                      static_cast<int>(n), 0, 31 + rbits, st));
+                                                      static_cast<int>(n), 0, cb + rbits, st));
         // last[row] = end of the row's entries; a max-scan into rowptr[1..M]
         // fills the rows without entries.
         DeviceBuffer last;
         RA_TRY(last.allocate(static_cast<size_t>(R) * sizeof(int32_t)));
         f32_fill_i32<<<grid_for(R), kThreads, 0, st>>>(last.get<int32_t>(), R, 0);
-        row_ends<<<grid_for(n), kThreads, 0, st>>>(keys2.get<uint64_t>(), n, last.get<int32_t>(),
+        row_ends<<<grid_for(n), kThreads, 0, st>>>(keys2.get<uint64_t>(), n, cb, last.get<int32_t>(),
                                                    p->f32_colind.get<int32_t>());
         RA_LAUNCH_CHECK("row_ends");
         size_t ms = 0;
