@@ -696,9 +696,14 @@ ra_status ra_zo_plan_create(const int32_t* h_rowptr, int32_t M, int32_t K, ra_zo
     if (!plan) return ra::fail(RA_ERR_OUT_OF_MEMORY, "zo: plan allocation");
     ra_status s = RA_OK;
     (void)hipGetDevice(&plan->device);
-    if ((s = plan->chunk_rows.upload(crow)) == RA_OK && (s = plan->chunk_starts.upload(cstart)) == RA_OK &&
-        (s = plan->chunk_slot.upload(slot)) == RA_OK && (s = plan->short_rows.upload(short_rows)) == RA_OK &&
-        (s = plan->split_rows.upload(split_rows)) == RA_OK && (s = plan->split_off.upload(split_off)) == RA_OK) {
+    auto up = [](int32_t* d, const std::vector<int32_t>& v) -> ra_status {
+        if (!v.empty()) RA_HIP_TRY(hipMemcpy(d, v.data(), v.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        return RA_OK;
+    };
+    if ((s = plan->carve(static_cast<int64_t>(short_rows.size()), z.num_chunks, z.num_split_rows)) == RA_OK &&
+        (s = up(plan->chunk_rows, crow)) == RA_OK && (s = up(plan->chunk_starts, cstart)) == RA_OK &&
+        (s = up(plan->chunk_slot, slot)) == RA_OK && (s = up(plan->short_rows, short_rows)) == RA_OK &&
+        (s = up(plan->split_rows, split_rows)) == RA_OK && (s = up(plan->split_off, split_off)) == RA_OK) {
         plan->info = z;
         plan->num_short_total = static_cast<int64_t>(short_rows.size());
         *out = plan;
@@ -737,15 +742,15 @@ ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
         if (vec)
             s = launch_zo<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
                                   reinterpret_cast<const float4*>(d_B), reinterpret_cast<float4*>(d_C),
-                                  plan->chunk_rows.get<int32_t>(), plan->chunk_starts.get<int32_t>(),
-                                  plan->chunk_slot.get<int32_t>(), plan->info.num_chunks,
-                                  plan->partials.get<float4>(), plan->short_rows.get<int32_t>(),
+                                  plan->chunk_rows, plan->chunk_starts,
+                                  plan->chunk_slot, plan->info.num_chunks,
+                                  plan->partials.get<float4>(), plan->short_rows,
                                   plan->num_short_total, np, np);
         else
             s = launch_zo<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
-                                 plan->chunk_rows.get<int32_t>(), plan->chunk_starts.get<int32_t>(),
-                                 plan->chunk_slot.get<int32_t>(), plan->info.num_chunks,
-                                 plan->partials.get<float>(), plan->short_rows.get<int32_t>(),
+                                 plan->chunk_rows, plan->chunk_starts,
+                                 plan->chunk_slot, plan->info.num_chunks,
+                                 plan->partials.get<float>(), plan->short_rows,
                                  plan->num_short_total, np, np);
         RA_TRY(s);
     }
@@ -754,12 +759,12 @@ ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
         const unsigned grid = static_cast<unsigned>((threads + kBlock - 1) / kBlock);
         if (vec)
             zo_merge_kernel<float4><<<grid, kBlock, 0, st>>>(
-                plan->split_rows.get<int32_t>(), plan->split_off.get<int32_t>(),
+                plan->split_rows, plan->split_off,
                 plan->partials.get<float4>(), reinterpret_cast<float4*>(d_C), np, np,
                 plan->info.num_split_rows);
         else
             zo_merge_kernel<float><<<grid, kBlock, 0, st>>>(
-                plan->split_rows.get<int32_t>(), plan->split_off.get<int32_t>(),
+                plan->split_rows, plan->split_off,
                 plan->partials.get<float>(), d_C, np, np, plan->info.num_split_rows);
         RA_LAUNCH_CHECK("zo_merge_kernel");
     }

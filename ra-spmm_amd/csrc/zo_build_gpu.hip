@@ -182,18 +182,10 @@ ra_status gpu_bin(ra_zo_plan* p, const int32_t* rowptr, int32_t M, int32_t K, hi
                    ((int64_t)z.num_small + z.num_empty + 3LL * z.num_chunks + 2LL * z.num_split_rows + 1);
     p->num_short_total = (int64_t)z.num_empty + z.num_small;
 
-    const auto i32 = sizeof(int32_t);
-    RA_TRY(p->short_rows.allocate(std::max<int64_t>(p->num_short_total, 1) * i32));
-    RA_TRY(p->chunk_rows.allocate(std::max(z.num_chunks, 1) * i32));
-    RA_TRY(p->chunk_starts.allocate(std::max(z.num_chunks, 1) * i32));
-    RA_TRY(p->chunk_slot.allocate(std::max(z.num_chunks, 1) * i32));
-    RA_TRY(p->split_rows.allocate(std::max(z.num_split_rows, 1) * i32));
-    RA_TRY(p->split_off.allocate((z.num_split_rows + 1) * i32));
+    RA_TRY(p->carve(p->num_short_total, z.num_chunks, z.num_split_rows));
     const int4 base{0, z.num_empty, z.num_empty + z.num_tiny, z.num_empty + z.num_tiny + z.num_short};
-    zo_scatter<<<grid_for(M), kThreads, 0, st>>>(rowptr, M, pre, base, p->short_rows.get<int32_t>(),
-                                                 p->chunk_rows.get<int32_t>(), p->chunk_starts.get<int32_t>(),
-                                                 p->chunk_slot.get<int32_t>(), p->split_rows.get<int32_t>(),
-                                                 p->split_off.get<int32_t>());
+    zo_scatter<<<grid_for(M), kThreads, 0, st>>>(rowptr, M, pre, base, p->short_rows, p->chunk_rows,
+                                                 p->chunk_starts, p->chunk_slot, p->split_rows, p->split_off);
     RA_LAUNCH_CHECK("zo_scatter");
     RA_HIP_TRY(hipStreamSynchronize(st));
     return RA_OK;
@@ -223,17 +215,17 @@ ra_status ra_zo_plan_export(const ra_zo_plan* p, const char* name, int32_t* dst,
     if (!p || !name || !count) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo export: NULL argument");
     const std::string n(name);
     const ra_zo_info& z = p->info;
-    const ra::DeviceBuffer* b = nullptr;
+    const int32_t* b = nullptr;
     int64_t c = 0;
-    if (n == "short_rows") { b = &p->short_rows; c = p->num_short_total; }
-    else if (n == "chunk_rows") { b = &p->chunk_rows; c = z.num_chunks; }
-    else if (n == "chunk_starts") { b = &p->chunk_starts; c = z.num_chunks; }
-    else if (n == "chunk_slot") { b = &p->chunk_slot; c = z.num_chunks; }
-    else if (n == "split_rows") { b = &p->split_rows; c = z.num_split_rows; }
-    else if (n == "split_off") { b = &p->split_off; c = z.M > 0 ? z.num_split_rows + 1 : 0; }
+    if (n == "short_rows") { b = p->short_rows; c = p->num_short_total; }
+    else if (n == "chunk_rows") { b = p->chunk_rows; c = z.num_chunks; }
+    else if (n == "chunk_starts") { b = p->chunk_starts; c = z.num_chunks; }
+    else if (n == "chunk_slot") { b = p->chunk_slot; c = z.num_chunks; }
+    else if (n == "split_rows") { b = p->split_rows; c = z.num_split_rows; }
+    else if (n == "split_off") { b = p->split_off; c = z.M > 0 ? z.num_split_rows + 1 : 0; }
     else return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo export: unknown array '" + n + "'");
     *count = c;
-    if (dst && c > 0) RA_HIP_TRY(hipMemcpy(dst, b->get(), c * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (dst && c > 0) RA_HIP_TRY(hipMemcpy(dst, b, c * sizeof(int32_t), hipMemcpyDeviceToHost));
     return RA_OK;
 }
 

@@ -6,6 +6,7 @@
 // chunk's row marks a sole chunk (rows of 65..256 nnz, written directly).
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
 
 #include "../../include/ra_spmm.h"
@@ -24,7 +25,27 @@ constexpr uint32_t kSoleFlag = 0x80000000u;
 struct ra_zo_plan {
     ra_zo_info info{};
     int device = 0;
-    ra::DeviceBuffer chunk_rows, chunk_starts, chunk_slot, short_rows, split_rows, split_off;
+    // The six lists live in one allocation (one hipMalloc per build, one
+    // hipFree per plan): short_rows | chunk_rows | chunk_starts | chunk_slot |
+    // split_rows | split_off, each 256-byte aligned.
+    ra::DeviceBuffer lists;
+    int32_t *short_rows = nullptr, *chunk_rows = nullptr, *chunk_starts = nullptr, *chunk_slot = nullptr,
+            *split_rows = nullptr, *split_off = nullptr;
     ra::DeviceBuffer partials;  // grown per N, reused across runs
     int64_t num_short_total = 0; // empty + tiny + short + medium
+
+    ra_status carve(int64_t n_short, int64_t n_chunks, int64_t n_split) {
+        const int64_t counts[6] = {n_short, n_chunks, n_chunks, n_chunks, n_split, n_split + 1};
+        auto round = [](int64_t n) { return (static_cast<size_t>(std::max<int64_t>(n, 1)) * 4 + 255) & ~size_t(255); };
+        size_t total = 0;
+        for (int64_t c : counts) total += round(c);
+        RA_TRY(lists.allocate(total));
+        int32_t** dst[6] = {&short_rows, &chunk_rows, &chunk_starts, &chunk_slot, &split_rows, &split_off};
+        size_t off = 0;
+        for (int i = 0; i < 6; ++i) {
+            *dst[i] = reinterpret_cast<int32_t*>(lists.get<char>() + off);
+            off += round(counts[i]);
+        }
+        return RA_OK;
+    }
 };
