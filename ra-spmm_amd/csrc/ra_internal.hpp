@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <cstdio>
 #include <functional>
 #include <string>
@@ -71,6 +72,14 @@ public:
     ra_status allocate(size_t bytes) {
         reset();
         if (bytes == 0) return RA_OK;
+        // RA_MAX_ALLOC_BYTES caps one allocation (read per call): a larger one
+        // fails as out of memory, so the failure paths can be exercised on a
+        // GPU with plenty of memory.
+        if (const char* cap = std::getenv("RA_MAX_ALLOC_BYTES")) {
+            if (bytes > std::strtoull(cap, nullptr, 10))
+                return fail(RA_ERR_OUT_OF_MEMORY, "hipMalloc: " + std::to_string(bytes) +
+                                                      " bytes exceed RA_MAX_ALLOC_BYTES");
+        }
         hipError_t e = hipMalloc(&ptr_, bytes);
         if (e != hipSuccess) {
             ptr_ = nullptr;

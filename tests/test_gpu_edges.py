@@ -93,3 +93,52 @@ def test_B_with_too_few_rows_is_rejected():
     t = ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, 32)
     with pytest.raises(RuntimeError, match="rows"):
         ra_spmm.run_tc_direct_plan(t, short)
+
+
+def test_allocation_failures_raise_cleanly_and_leak_nothing(monkeypatch):
+    """Failure taxonomy (the OOM case): with RA_MAX_ALLOC_BYTES capping every
+    library allocation, each plan build and each run that grows plan scratch
+    raises RuntimeError (RA_ERR_OUT_OF_MEMORY); the plans stay usable once the
+    cap is lifted.  Repeating the whole cycle leaves device memory outside
+    torch's caching allocator unchanged (the first cycle absorbs one-time
+    runtime allocations)."""
+    from ra_spmm import synthetic as S
+    g = S.random_csr(6000, 6000, 14.0, seed=31, skew=0.9, max_deg=3000)
+    assert int(np.diff(g.rowptr).max()) > 512  # split ZO chunks: partial slots are allocated per N
+    rp, ci, vl = g.torch("cuda")
+    B = torch.randn(g.K, 64, device="cuda")
+    ref = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
+    scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
+    makers = [lambda: ra_spmm.make_zero_overhead_plan(rp, g.M, g.K),
+              lambda: ra_spmm.make_zero_overhead_plan(rp.cpu(), g.M, g.K, build="host"),
+              lambda: ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, 64),
+              lambda: ra_spmm.make_community_tc_plan(rp.cpu(), ci.cpu(), vl.cpu(), g.M, g.K, 64, build="host")]
+
+    def cycle():
+        monkeypatch.setenv("RA_MAX_ALLOC_BYTES", "4096")
+        for mk in makers:
+            with pytest.raises(RuntimeError, match="RA_ERR_OUT_OF_MEMORY"):
+                mk()
+        monkeypatch.delenv("RA_MAX_ALLOC_BYTES")
+        zo, tc = makers[0](), makers[2]()
+        monkeypatch.setenv("RA_MAX_ALLOC_BYTES", "4096")
+        with pytest.raises(RuntimeError, match="RA_ERR_OUT_OF_MEMORY"):
+            ra_spmm.run_zero_overhead_plan(zo, rp, ci, vl, B)       # partial slots
+        with pytest.raises(RuntimeError, match="RA_ERR_OUT_OF_MEMORY"):
+            ra_spmm.run_tc_direct_plan(tc, B)                      # fp16 copy of B
+        with pytest.raises(RuntimeError, match="RA_ERR_OUT_OF_MEMORY"):
+            ra_spmm.run_tc_direct_plan_tf32(tc, B)                 # CSR of the stored values
+        monkeypatch.delenv("RA_MAX_ALLOC_BYTES")
+        assert bool(((ra_spmm.run_zero_overhead_plan(zo, rp, ci, vl, B) - ref).abs() <= 1e-5 * scale + 1e-30).all())
+        # FP32 route: exact products of the fp16-rounded values (2^-11 relative each).
+        assert bool(((ra_spmm.run_tc_direct_plan_tf32(tc, B) - ref).abs() <= 2.0 ** -10 * scale + 1e-30).all())
+        assert bool(ra_spmm.run_tc_direct_plan(tc, B).isfinite().all())
+        del zo, tc
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return torch.cuda.mem_get_info()[0] + torch.cuda.memory_reserved()
+
+    free0 = cycle()
+    for _ in range(3):
+        free1 = cycle()
+    assert abs(free1 - free0) < (2 << 20), (free0, free1)
