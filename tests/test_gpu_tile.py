@@ -163,7 +163,8 @@ def test_c4_full_size_properties(oracle):
     """config C4 (log-normal degrees to 20k, fp16 values) at full size through
     the routed COMMUNITY_TC and TC_DIRECT with the automatic 8 column
     partitions: a row sample (including the 20 longest rows) against the
-    oracle at N=512, and the all-ones row sums on every row."""
+    oracle at N=512 on the FP16 route (1e-5) and the FP32 route (bit-exact),
+    and the all-ones row sums on every row."""
     g = S.CONFIGS["C4"]()
     gd = g.torch("cuda")
     N = 512
@@ -186,6 +187,10 @@ def test_c4_full_size_properties(oracle):
         C = run(kind, plan, Bd, "f16", gd)
         assert_close_scaled(C.cpu().numpy()[rows], ref, scale, 1e-5, f"C4 kind {kind}")
         del C
+        # FP32 route over the 8 column ranges: one fma chain per element in
+        # ascending column order (values are fp16-representable: stored exactly).
+        C32 = run(kind, plan, Bd, "fp32", gd).cpu().numpy()[rows]
+        np.testing.assert_array_equal(C32, oracle.spmm_seq_f32(sub_rp, sub_ci, sub_vl, B), err_msg=f"C4 fp32 {kind}")
         ones = torch.ones(g.K, 16, device="cuda")
         rs = run(kind, plan, ones, "f16", gd)[:, 0].double().cpu().numpy()
         assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
