@@ -59,7 +59,7 @@ constexpr RouterTable kReference = {
 // MI355X calibration (structure of the tree unchanged; measured on gfx950 with
 // bench.py --sweep over the five benchmark configs C1-C5):
 //  - tile gate: the device tile build (sorts and scans on the GPU) runs at
-//    1.3-1.9e-10 s per nnz (C2 1.6e7 nnz: 3.0 ms; C4 1.24e8 nnz: 15.8 ms),
+//    1.0-1.9e-10 s per nnz (C2 1.6e7 nnz: 2.8 ms; C4 1.24e8 nnz: 12.7 ms),
 //    plus ~3e-10 s per nnz to upload a host CSR (the host builder took
 //    0.75-1.5e-8 s per nnz), so the estimate is 1e-9 s per nnz with the same
 //    20 s budget;

@@ -144,6 +144,32 @@ __global__ void entry_keys(const int32_t* __restrict__ row_of, const int32_t* __
     }
 }
 
+// Window-height sampling: flag[t] = 1 when nonzero t lies in a sampled
+// 32-row window (every S-th), and the sampled keys (32-row windows, sb = 5)
+// written compactly at the exclusive-scan offsets of the flags.
+__global__ void sample_flags(const int32_t* __restrict__ row_of, const int32_t* __restrict__ pos, int64_t n, int S,
+                             int32_t* __restrict__ flag) {
+    RA_GRID_STRIDE(t, n) {
+        const int lo = row_of[t];
+        const int64_t slot_pos = pos ? pos[lo] : lo;
+        flag[t] = ((slot_pos >> 5) % S) == 0 ? 1 : 0;
+    }
+}
+
+__global__ void sampled_keys(const int32_t* __restrict__ row_of, const int32_t* __restrict__ colind,
+                             const int32_t* __restrict__ pos, int64_t base, int64_t n, int cb, int S,
+                             const int32_t* __restrict__ off, uint64_t* __restrict__ keys) {
+    RA_GRID_STRIDE(t, n) {
+        const int lo = row_of[t];
+        const int64_t slot_pos = pos ? pos[lo] : lo;
+        const int64_t w = slot_pos >> 5;
+        if (w % S != 0) continue;
+        keys[off[t]] = (static_cast<uint64_t>(w) << (cb + 5)) |
+                       (static_cast<uint64_t>(static_cast<uint32_t>(colind[base + t])) << 5) |
+                       static_cast<uint64_t>(slot_pos & 31);
+    }
+}
+
 __global__ void mark_new(const uint64_t* __restrict__ keys, int64_t n, int sb, int32_t* __restrict__ newvec,
                          int32_t* __restrict__ newkey) {
     RA_GRID_STRIDE(i, n) {
@@ -363,6 +389,9 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     size_t red2 = 0;
     RA_HIP_TRY(hipcub::DeviceReduce::Sum(nullptr, red2, inull, inull, static_cast<int>(nn), st));
     red_bytes = std::max(red_bytes, red2);
+    size_t scan5 = 0;
+    RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, scan5, inull, inull, static_cast<int>(nn), st));
+    scan_bytes = std::max(scan_bytes, scan5);
     size_t scan4 = 0;
     RA_HIP_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, scan4, inull, inull, hipcub::Max(), static_cast<int>(nn),
                                                  st));
@@ -448,20 +477,42 @@ ra_status gpu_build(ra_tile_plan* p, int32_t kind, const int32_t* rowptr, const 
     if (rows == 0) {
         rows = ra::kTileWindow;
         if (n > 0) {
+            // Counts from every S-th 32-row window (S a power of two <= 16,
+            // at least 2^21 sampled nonzeros and 512 sampled windows): the
+            // counts estimate the full ones up to the factor S, and sorting
+            // 1/S of the keys costs 1/S of the sort.  Deterministic.
+            const int64_t W32 = (M + 31) / 32;
+            int S = 1;
+            while (S < 16 && n / (2 * S) >= (int64_t(1) << 21) && W32 / (2 * S) >= 512) S *= 2;
+            int64_t ns = n;
             fill_u32<<<1, kThreads, 0, st>>>(reinterpret_cast<unsigned*>(layout_counts), 6);
-            entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, 5, cb, INT32_MAX,
-                                                         (M + 31) / 32, keys, nullptr);
+            if (S == 1) {
+                entry_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, vals, pos_ptr, base, n, 5, cb, INT32_MAX,
+                                                             W32, keys, nullptr);
+            } else {
+                sample_flags<<<grid_for(n), kThreads, 0, st>>>(row_of, pos_ptr, n, S, newvec);
+                size_t tb = tmp_bytes;
+                RA_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(tmp, tb, newvec, vid, static_cast<int>(n), st));
+                sampled_keys<<<grid_for(n), kThreads, 0, st>>>(row_of, colind, pos_ptr, base, n, cb, S, vid, keys);
+                int32_t last[2];
+                RA_TRY(read_back(&last[0], vid + n - 1, 1, st));
+                RA_TRY(read_back(&last[1], newvec + n - 1, 1, st));
+                ns = static_cast<int64_t>(last[0]) + last[1];
+            }
+            RA_LAUNCH_CHECK("height sample keys");
             int wb = 0;
-            while ((int64_t(1) << wb) < (M + 31) / 32) ++wb;
-            size_t tb = tmp_bytes;
-            RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, keys, keys2, static_cast<int>(n), 0, 5 + cb + wb,
-                                                         st));
-            count_layouts<<<std::min<unsigned>(grid_for(n), kReduceBlocks), kThreads, 0, st>>>(keys2, n,
-                                                                                                layout_counts);
-            RA_LAUNCH_CHECK("count_layouts");
+            while ((int64_t(1) << wb) < W32) ++wb;
+            if (ns > 0) {
+                size_t tb = tmp_bytes;
+                RA_HIP_TRY(hipcub::DeviceRadixSort::SortKeys(tmp, tb, keys, keys2, static_cast<int>(ns), 0,
+                                                             5 + cb + wb, st));
+                count_layouts<<<std::min<unsigned>(grid_for(ns), kReduceBlocks), kThreads, 0, st>>>(keys2, ns,
+                                                                                                     layout_counts);
+                RA_LAUNCH_CHECK("count_layouts");
+            }
             unsigned long long v[3];
             RA_TRY(read_back(v, layout_counts, 3, st));
-            rows = choose_rows(v[0], v[1], v[2], M);
+            rows = choose_rows(v[0] * S, v[1] * S, v[2] * S, M);
         }
     }
     if (rows != 8 && rows != 16 && rows != 32)
