@@ -115,3 +115,36 @@ def test_auto_height_follows_column_sharing():
         assert (p.rows_per_window > 8) == tall, (g.name, p.rows_per_window)
     with pytest.raises(RuntimeError):
         ra_spmm.make_tc_direct_plan(rp.cpu(), ci.cpu(), vl.cpu(), g.M, g.K, 128, build="host", rows_per_window=32)
+
+
+def _model_rows(g):
+    """The height the build's cost model picks from exact distinct (row / h,
+    column) counts: 10 per 32 vectors at h = 8 and 16, 11 at h = 32, a tall
+    layout only when it saves >= 15%."""
+    rows = np.repeat(np.arange(g.M, dtype=np.int64), np.diff(g.rowptr.astype(np.int64)))
+    c = g.colind.astype(np.int64)
+    v = {h: np.unique((rows // h) * g.K + c).size for h in (8, 16, 32)}
+    c8, c16, c32 = 10.0 * v[8], 10.0 * v[16], 11.0 * v[32]
+    if c32 <= 0.85 * c8 and c32 <= c16:
+        return 32
+    if c16 <= 0.85 * c8:
+        return 16
+    return 8
+
+
+@pytest.mark.parametrize("gname", ["sbm_large", "random_large", "mixed_large", "mixed_weak"])
+def test_sampled_height_matches_exact_model(gname):
+    """Large matrices count vectors on every S-th 32-row window only; the
+    height chosen equals the exact model's on community, random and mixed
+    graphs."""
+    graphs = {
+        "sbm_large": lambda: S.sbm(512, 128, 96.0, 0.9, seed=12),            # 65k rows, 5.4M nnz
+        "random_large": lambda: S.random_csr(70000, 300000, 80.0, seed=13),   # 5.6M nnz
+        "mixed_large": lambda: S.sbm(1024, 96, 60.0, 0.7, seed=14),          # weaker communities (model: 0.78)
+        "mixed_weak": lambda: S.sbm(1024, 96, 60.0, 0.4, seed=14),           # model: 0.92 -> 8 rows
+    }
+    g = graphs[gname]()
+    assert g.nnz >= (1 << 21) * 2  # sampling is on (S >= 2)
+    rp, ci, vl = g.torch("cuda")
+    p = ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, 128)
+    assert p.rows_per_window == _model_rows(g), (gname, p.rows_per_window)
