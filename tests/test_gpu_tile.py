@@ -196,3 +196,23 @@ def test_c4_full_size_properties(oracle):
         assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
         del plan
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("N", [1024, 2000])
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_wide_B(oracle, kind, N):
+    """Many column slices: N=1024 (8 slices of 128, slice-major order with
+    the window remap) and N=2000 (not a multiple of 8: B is padded to ldb in
+    the fp16 copy, the tail columns are masked)."""
+    g = GRAPHS["skewed"]()
+    gd = g.torch("cuda")
+    B = np.random.default_rng(N + kind).standard_normal((g.K, N)).astype(np.float32)
+    Bd = torch.from_numpy(B).cuda()
+    plan = MAKE[kind](gd[0], gd[1], gd[2], g.M, g.K, N)
+    C = run(kind, plan, Bd, "f16", gd).cpu().numpy()
+    qv, qb = oracle.quantize_f16(g.vals), oracle.quantize_f16(B)
+    assert_close_scaled(C, oracle.spmm_tile_f64(g.rowptr, g.colind, g.vals, B, "f16"),
+                        oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5, f"wide f16 N={N}")
+    qs = oracle.quantize_f16_scaled(g.vals, oracle.tile_value_scale_log2(g.vals))
+    assert_fp32_route(run(kind, plan, Bd, "fp32", gd).cpu().numpy(), g.rowptr, g.colind, qs, B, oracle,
+                      f"wide fp32 N={N}")
