@@ -271,7 +271,6 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
     item_range(it, item, w, b0, b1, slot);
     const int j = lane & 15;
     const int q = lane >> 4;
-    const int h = j & 1;
     const int col = slice * (16 * CPL) + j * CPL;
     const bool col_ok = col < ldb;
 
@@ -281,27 +280,39 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc) acc[g][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto load_step = [&](int b, int (&cols)[8], u16x8 (&a)[RG]) {
-        const int4 mine = *reinterpret_cast<const int4*>(atox + (int64_t)b * 32 + q * 8 + h * 4);
+    // Column indices come 8 blocks at a time: one 16-byte load per lane
+    // covers the 256 indices of blocks [c0, c0 + 8) (lane L: indices 4L..4L+3),
+    // and step b takes its 8 from lanes 8s + 2q and 8s + 2q + 1 (s = b - c0)
+    // by lane permutes, which use the LDS unit, not the address unit.
+    auto load_chunk = [&](int c0) {
+        int4 v = make_int4(-1, -1, -1, -1);
+        if (c0 + (lane >> 3) < b1) v = *reinterpret_cast<const int4*>(atox + (int64_t)c0 * 32 + lane * 4);
+        return v;
+    };
+    auto cols_of = [&](const int4& chunk, int s, int (&cols)[8]) {
+        const int l0 = 8 * s + 2 * q;
+        cols[0] = __shfl(chunk.x, l0, kWave);
+        cols[1] = __shfl(chunk.y, l0, kWave);
+        cols[2] = __shfl(chunk.z, l0, kWave);
+        cols[3] = __shfl(chunk.w, l0, kWave);
+        cols[4] = __shfl(chunk.x, l0 + 1, kWave);
+        cols[5] = __shfl(chunk.y, l0 + 1, kWave);
+        cols[6] = __shfl(chunk.z, l0 + 1, kWave);
+        cols[7] = __shfl(chunk.w, l0 + 1, kWave);
+    };
+    auto load_a = [&](int b, u16x8 (&a)[RG]) {
 #pragma unroll
         for (int g = 0; g < RG; ++g)
             a[g] = *reinterpret_cast<const u16x8*>(vals + (int64_t)b * BV + ((g * 4 + q) * 16 + j) * 8);
-        int4 other;
-        other.x = __shfl_xor(mine.x, 1, kWave);
-        other.y = __shfl_xor(mine.y, 1, kWave);
-        other.z = __shfl_xor(mine.z, 1, kWave);
-        other.w = __shfl_xor(mine.w, 1, kWave);
-        const int4 lo = h ? other : mine, hi = h ? mine : other;
-        cols[0] = lo.x; cols[1] = lo.y; cols[2] = lo.z; cols[3] = lo.w;
-        cols[4] = hi.x; cols[5] = hi.y; cols[6] = hi.z; cols[7] = hi.w;
     };
-    int cols_next[8];
+    int4 chunk = load_chunk(b0), chunk_next = make_int4(-1, -1, -1, -1);
     u16x8 a_next[RG];
-    if (b0 < b1) load_step(b0, cols_next, a_next);
+    if (b0 < b1) load_a(b0, a_next);
     for (int b = b0; b < b1; ++b) {
+        const int s = (b - b0) & 7;
+        if (s == 0 && b + 8 < b1) chunk_next = load_chunk(b + 8);  // one chunk ahead
         int cols[8];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) cols[v] = cols_next[v];
+        cols_of(chunk, s, cols);
         u16x8 a[RG];
 #pragma unroll
         for (int g = 0; g < RG; ++g) a[g] = a_next[g];
@@ -313,7 +324,8 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
             else
                 raw[v] = Run{};
         }
-        if (b + 1 < b1) load_step(b + 1, cols_next, a_next);
+        if (b + 1 < b1) load_a(b + 1, a_next);
+        if (s == 7) chunk = chunk_next;
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc) {
             u16x8 bop;
