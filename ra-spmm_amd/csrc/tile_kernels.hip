@@ -159,35 +159,37 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
 #pragma unroll
     for (int cc = 0; cc < CPL; ++cc) acc[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Indices and A fragment of step b (block b+q of this lane group).  Every
-    // vector-memory instruction costs the same address-unit time whatever its
-    // width, so lane pairs (j, j^1) each load half of the block's 8 indices
-    // with one 16-byte load and swap halves through a lane exchange.
-    const int h = j & 1;
-    auto load_step = [&](int b, int (&cols)[8], u16x8& a) {
-        const int bq = b + q;
-        int4 mine = make_int4(-1, -1, -1, -1);
-        a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (bq < b1) {
-            mine = *reinterpret_cast<const int4*>(atox + (int64_t)bq * 8 + h * 4);
-            if (a_half) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)bq * 64 + (j & 7) * 8);
-        }
-        int4 other;
-        other.x = __shfl_xor(mine.x, 1, kWave);
-        other.y = __shfl_xor(mine.y, 1, kWave);
-        other.z = __shfl_xor(mine.z, 1, kWave);
-        other.w = __shfl_xor(mine.w, 1, kWave);
-        const int4 lo = h ? other : mine, hi = h ? mine : other;
-        cols[0] = lo.x; cols[1] = lo.y; cols[2] = lo.z; cols[3] = lo.w;
-        cols[4] = hi.x; cols[5] = hi.y; cols[6] = hi.z; cols[7] = hi.w;
+    // Column indices come 32 blocks (8 steps) at a time: one 16-byte load per
+    // lane (lane L: indices 4L..4L+3, half L&1 of block c0 + L/2), handed to
+    // step s's lane group q (block c0 + 4s + q) from lanes 8s + 2q and
+    // 8s + 2q + 1 by lane permutes, which use the LDS unit, not the address
+    // unit.  The A fragment of block b+q is loaded one step ahead.
+    auto load_chunk = [&](int c0) {
+        int4 v = make_int4(-1, -1, -1, -1);
+        if (c0 + (lane >> 1) < b1) v = *reinterpret_cast<const int4*>(atox + (int64_t)c0 * 8 + lane * 4);
+        return v;
     };
-    int cols_next[8];
-    u16x8 a_next;
-    if (b0 < b1) load_step(b0, cols_next, a_next);
+    auto load_a = [&](int b) {
+        u16x8 a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (b + q < b1 && a_half) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)(b + q) * 64 + (j & 7) * 8);
+        return a;
+    };
+    int4 chunk = load_chunk(b0), chunk_next = make_int4(-1, -1, -1, -1);
+    u16x8 a_next = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (b0 < b1) a_next = load_a(b0);
     for (int b = b0; b < b1; b += 4) {
+        const int s = ((b - b0) >> 2) & 7;
+        if (s == 0 && b + 32 < b1) chunk_next = load_chunk(b + 32);  // one chunk ahead
+        const int l0 = 8 * s + 2 * q;
         int cols[8];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) cols[v] = cols_next[v];
+        cols[0] = __shfl(chunk.x, l0, kWave);
+        cols[1] = __shfl(chunk.y, l0, kWave);
+        cols[2] = __shfl(chunk.z, l0, kWave);
+        cols[3] = __shfl(chunk.w, l0, kWave);
+        cols[4] = __shfl(chunk.x, l0 + 1, kWave);
+        cols[5] = __shfl(chunk.y, l0 + 1, kWave);
+        cols[6] = __shfl(chunk.z, l0 + 1, kWave);
+        cols[7] = __shfl(chunk.w, l0 + 1, kWave);
         const u16x8 a = a_next;
         Run raw[8];
 #pragma unroll
@@ -197,9 +199,8 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
             else
                 raw[v] = Run{};
         }
-        // Prefetch the next step's indices while this step's gathers are in
-        // flight: the atox -> B dependency leaves the critical path.
-        if (b + 4 < b1) load_step(b + 4, cols_next, a_next);
+        if (b + 4 < b1) a_next = load_a(b + 4);
+        if (s == 7) chunk = chunk_next;
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc) {
             u16x8 bop;
