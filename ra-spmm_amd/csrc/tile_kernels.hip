@@ -41,6 +41,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <int CPL> struct HalfRun;  // CPL contiguous 16-bit elements
 template <> struct HalfRun<1> { typedef unsigned short T; };
@@ -163,22 +164,27 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
     // lane (lane L: indices 4L..4L+3, half L&1 of block c0 + L/2), handed to
     // step s's lane group q (block c0 + 4s + q) from lanes 8s + 2q and
     // 8s + 2q + 1 by lane permutes, which use the LDS unit, not the address
-    // unit.  The A fragment of block b+q is loaded one step ahead.
+    // unit.  A fragments come two steps per load: lane j needs block b+q's
+    // row j&7 on even steps when a_half, and its partner lane j^8 (same q and
+    // row, !a_half) loads the same row of block b+4+q, handed over on the odd
+    // step by a lane exchange.  The pair is loaded one step ahead.
     auto load_chunk = [&](int c0) {
         int4 v = make_int4(-1, -1, -1, -1);
         if (c0 + (lane >> 1) < b1) v = *reinterpret_cast<const int4*>(atox + (int64_t)c0 * 8 + lane * 4);
         return v;
     };
-    auto load_a = [&](int b) {
+    auto load_pair = [&](int b) {  // b = first block of an even step
+        const int blk = b + q + (a_half ? 0 : 4);
         u16x8 a = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (b + q < b1 && a_half) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)(b + q) * 64 + (j & 7) * 8);
+        if (blk < b1) a = *reinterpret_cast<const u16x8*>(vals + (int64_t)blk * 64 + (j & 7) * 8);
         return a;
     };
     int4 chunk = load_chunk(b0), chunk_next = make_int4(-1, -1, -1, -1);
-    u16x8 a_next = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (b0 < b1) a_next = load_a(b0);
+    u16x8 apair = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (b0 < b1) apair = load_pair(b0);
     for (int b = b0; b < b1; b += 4) {
-        const int s = ((b - b0) >> 2) & 7;
+        const int t = (b - b0) >> 2;
+        const int s = t & 7;
         if (s == 0 && b + 32 < b1) chunk_next = load_chunk(b + 32);  // one chunk ahead
         const int l0 = 8 * s + 2 * q;
         int cols[8];
@@ -190,7 +196,19 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
         cols[5] = __shfl(chunk.y, l0 + 1, kWave);
         cols[6] = __shfl(chunk.z, l0 + 1, kWave);
         cols[7] = __shfl(chunk.w, l0 + 1, kWave);
-        const u16x8 a = a_next;
+        u16x8 a;
+        if ((t & 1) == 0) {
+            a = a_half ? apair : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        } else {
+            // The partner's register holds this step's row of block b+q.
+            const u32x4 w = __builtin_bit_cast(u32x4, apair);
+            u32x4 o;
+            o[0] = __shfl_xor(w[0], 8, kWave);
+            o[1] = __shfl_xor(w[1], 8, kWave);
+            o[2] = __shfl_xor(w[2], 8, kWave);
+            o[3] = __shfl_xor(w[3], 8, kWave);
+            a = a_half ? __builtin_bit_cast(u16x8, o) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
         Run raw[8];
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
@@ -199,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
             else
                 raw[v] = Run{};
         }
-        if (b + 4 < b1) a_next = load_a(b + 4);
+        if ((t & 1) == 1 && b + 4 < b1) apair = load_pair(b + 4);
         if (s == 7) chunk = chunk_next;
 #pragma unroll
         for (int cc = 0; cc < CPL; ++cc) {
