@@ -1,10 +1,12 @@
 """Seeded random matrices through every path, each against its bar:
   CSR_DIRECT, baseline            bit-identical to the oracle's fma chain
+  fp16 guardrail                  bit-identical to the chain on fp16-rounded A values and B
   ZERO_OVERHEAD_CSR               rows <= 64 nnz bit-identical, all within 1e-5 of |A||B|
   tile FP16 route (any layout)    1e-5 of |Aq||Bq| against fp64 of the quantised inputs
   tile FP32 route (any layout)    1e-5 of |Aq||B| against fp64 of the stored values
 Shapes, densities, skew, empty rows, duplicate entries, N (1..300, ragged),
-window heights and column partitions vary with the seed."""
+window heights, column partitions and the stored value type (fp16 / bf16)
+vary with the seed."""
 import os
 
 import numpy as np
@@ -37,7 +39,7 @@ def _graph(rng):
     return g
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_parity(oracle, seed):
     rng = np.random.default_rng(1000 + seed)
     g = _graph(rng)
@@ -51,6 +53,9 @@ def test_random_parity(oracle, seed):
     scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B))
     np.testing.assert_array_equal(ra_spmm.spmm_csr_direct(rp, ci, vl, Bd).cpu().numpy(), seq)
     np.testing.assert_array_equal(ra_spmm.spmm_csr_baseline(rp, ci, vl, Bd).cpu().numpy(), seq)
+    np.testing.assert_array_equal(
+        ra_spmm.spmm_cusparse_fp16(rp, ci, vl, Bd).cpu().numpy(),
+        oracle.spmm_seq_f32(g.rowptr, g.colind, oracle.quantize_f16(g.vals), oracle.quantize_f16(B)))
     z = ra_spmm.make_zero_overhead_plan(rp, g.M, g.K)
     C = ra_spmm.run_zero_overhead_plan(z, rp, ci, vl, Bd).cpu().numpy()
     short = np.diff(g.rowptr) <= 64
@@ -60,19 +65,23 @@ def test_random_parity(oracle, seed):
         return
     rows = int(rng.choice([0, 8, 16, 32]))
     parts = str(int(rng.choice([1, 1, 2, 8])))
-    qv, qb = oracle.quantize_f16(g.vals), oracle.quantize_f16(B)
+    vdt = "bf16" if rng.random() < 0.25 else "fp16"
+    quant = oracle.quantize_bf16 if vdt == "bf16" else oracle.quantize_f16
+    qv, qb = quant(g.vals), quant(B)
     mrp, mci, mvl = oracle.merge_duplicates(g.rowptr, g.colind, g.vals)  # what a plan stores
-    qs = oracle.quantize_f16_scaled(mvl, oracle.tile_value_scale_log2(g.vals))
+    qs = (oracle.quantize_bf16(mvl) if vdt == "bf16"
+          else oracle.quantize_f16_scaled(mvl, oracle.tile_value_scale_log2(g.vals)))
     old = os.environ.get("RA_TILE_COL_PARTS")
     os.environ["RA_TILE_COL_PARTS"] = parts
     try:
         for kind, mk in enumerate((ra_spmm.make_tc_direct_plan, ra_spmm.make_community_tc_plan,
                                    ra_spmm.make_segment_hybrid_plan)):
-            p = mk(rp, ci, vl, g.M, g.K, N, rows_per_window=rows)
-            C16 = ra_spmm.run_tile_plan_route(p, Bd, "fp16").cpu().numpy()
-            assert_close_scaled(C16, oracle.spmm_tile_f64(g.rowptr, g.colind, g.vals, B, "f16"),
+            p = mk(rp, ci, vl, g.M, g.K, N, vdt, rows_per_window=rows)
+            C16 = ra_spmm.run_tile_plan_route(p, Bd, vdt).cpu().numpy()
+            assert_close_scaled(C16, oracle.spmm_tile_f64(g.rowptr, g.colind, g.vals, B,
+                                                          "bf16" if vdt == "bf16" else "f16"),
                                 oracle.spmm_f64(g.rowptr, g.colind, np.abs(qv), np.abs(qb)), 1e-5,
-                                f"tile f16 kind={kind} rows={p.rows_per_window} parts={p.col_parts}")
+                                f"tile {vdt} kind={kind} rows={p.rows_per_window} parts={p.col_parts}")
             C32 = ra_spmm.run_tile_plan_route(p, Bd, "fp32").cpu().numpy()
             assert_fp32_route(C32, mrp, mci, qs, B, oracle,
                               f"tile fp32 kind={kind} rows={p.rows_per_window} parts={p.col_parts}")
