@@ -308,6 +308,24 @@ def bench_gcn(steps, warmup, table, backends=("router", "cusparse", "zero_overhe
             f"{rec.get('paths', '')}")
         del graph, model, opt
         torch.cuda.empty_cache()
+    if "router" in backends:
+        # The same model with order="auto": layer 1 aggregates before its
+        # linear map (SpMM at N=128, no backward SpMM).  Reported beside the
+        # reference-order step, never in its place.
+        torch.manual_seed(1)
+        graph = gnn.GraphBackend(op, "cuda", table)
+        model = gnn.GCN(128, 256, 47, order="auto").cuda()
+        opt = torch.optim.Adam(model.parameters(), lr=1e-2)
+        cold = gnn.train_step(model, graph, "router", X, y, opt)
+        for _ in range(warmup):
+            gnn.train_step(model, graph, "router", X, y, opt)
+        ts = [gnn.train_step(model, graph, "router", X, y, opt) for _ in range(steps)]
+        ms = 1e3 * sum(ts) / len(ts)
+        out["router_order_auto"] = {"step_ms": ms, "cold_first_step_ms": cold * 1e3,
+                                    "spmm_flops_per_step": 2.0 * g.nnz * (128 + 47 + 47)}
+        log(f"[gcn] router order=auto step {ms:8.3f} ms  cold first step {cold * 1e3:9.1f} ms")
+        del graph, model, opt
+        torch.cuda.empty_cache()
     return out
 
 

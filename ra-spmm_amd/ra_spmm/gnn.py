@@ -293,17 +293,33 @@ class Linear(nn.Linear):
 class GCN(nn.Module):
     """2-layer GCN: A relu(A X W1) W2 (gnn_bench/router_vs_baselines_gcn.py:464-476).
     The linear layers are bias-free nn.Linear, as in the reference, with the
-    chunked weight-gradient reduction."""
+    chunked weight-gradient reduction.
 
-    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int):
+    order="reference" (default) transforms before aggregating in both layers,
+    as the reference does: A (X W1), then A (H W2).  order="auto" aggregates
+    first where a layer widens (in_features < out_features), the rule DGL's
+    GraphConv uses: (A X) W1 is the same product with the SpMM at the input
+    width (128 instead of 256 for config 5), and since X needs no gradient
+    the layer's backward A^T SpMM disappears.  The results agree to fp32
+    rounding; the reference's SpMM count per step is kept only by the
+    default."""
+
+    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int, order: str = "reference"):
         super().__init__()
+        if order not in ("reference", "auto"):
+            raise ValueError(f"order must be 'reference' or 'auto', got {order!r}")
+        self.order = order
         self.lin1 = Linear(in_dim, hidden_dim)
         self.lin2 = Linear(hidden_dim, out_dim)
 
+    def _layer(self, lin, x, graph, backend):
+        if self.order == "auto" and lin.in_features < lin.out_features:
+            return lin(SparseMMFunction.apply(x, graph, backend))
+        return SparseMMFunction.apply(lin(x), graph, backend)
+
     def forward(self, X, graph: GraphBackend, backend: str):
-        h = SparseMMFunction.apply(self.lin1(X), graph, backend)
-        h = F.relu(h)
-        return SparseMMFunction.apply(self.lin2(h), graph, backend)[:, :self.lin2.out_features]
+        h = F.relu(self._layer(self.lin1, X, graph, backend))
+        return self._layer(self.lin2, h, graph, backend)[:, :self.lin2.out_features]
 
 
 GCNBench = GCN

@@ -77,3 +77,12 @@ def test_chunked_weight_grad_and_linear(monkeypatch):
     (ref_lin(xr) ** 2).sum().backward()
     torch.testing.assert_close(lin.weight.grad, ref_lin.weight.grad)
     torch.testing.assert_close(xi.grad, xr.grad)
+
+
+def test_gcn_order_argument():
+    import pytest
+    from ra_spmm import gnn
+    assert gnn.GCN(4, 8, 3).order == "reference"
+    assert gnn.GCN(4, 8, 3, order="auto").order == "auto"
+    with pytest.raises(ValueError):
+        gnn.GCN(4, 8, 3, order="aggregate")

@@ -62,6 +62,33 @@ def test_gcn_step_matches_dense_reference():
             torch.testing.assert_close(g_, r_, rtol=10 * rtol, atol=atol, msg=backend)
 
 
+def test_gcn_order_auto_matches_dense_reference():
+    """order="auto": layer 1 (32 -> 64) aggregates first, (A X) W1, and runs
+    no backward SpMM for it; same outputs and gradients as the dense model."""
+    op = _operator(3000, seed=5)
+    M = op.shape[0]
+    torch.manual_seed(0)
+    X = torch.randn(M, 32, device="cuda")
+    y = torch.randint(0, 7, (M,), device="cuda")
+    dense = torch.from_numpy(op.toarray()).cuda()
+    torch.manual_seed(1)
+    model = gnn.GCN(32, 64, 7, order="auto").cuda()
+    graph = gnn.GraphBackend(op, "cuda")
+    out = model(X, graph, "zero_overhead")
+    F.cross_entropy(out, y).backward()
+    # forward at widths 32 (layer 1, aggregated first) and 8 (layer 2, padded
+    # 7), backward only for layer 2
+    assert sorted((t, n) for (_, t, n) in graph.exec_cache) == [(False, 8), (False, 32), (True, 8)]
+    torch.manual_seed(1)
+    ref_model = gnn.GCN(32, 64, 7).cuda()
+    h = F.relu(dense @ F.linear(X, ref_model.lin1.weight))
+    ref_out = dense @ F.linear(h, ref_model.lin2.weight)
+    F.cross_entropy(ref_out, y).backward()
+    torch.testing.assert_close(out, ref_out, rtol=2e-4, atol=2e-5)
+    for p, r in zip(model.parameters(), ref_model.parameters()):
+        torch.testing.assert_close(p.grad, r.grad, rtol=2e-3, atol=2e-5)
+
+
 def test_router_plans_per_transpose_and_width():
     op = _operator(5000, seed=7)
     graph = gnn.GraphBackend(op, "cuda")
