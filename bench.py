@@ -241,6 +241,22 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
         "speedup_vs_baseline": base_wall / wall_ms,
         "max_rel_err_vs_baseline": max_rel,
     }
+    if label in ra_spmm.TILE_KERNELS and not label.endswith("_TF32") and N % 8 == 0:
+        # Native 16-bit B (the fp16-B configs C3 and C4): the same plan run on
+        # B already in fp16, with no per-call conversion pass; bytes_alg then
+        # counts 2-byte B and stored values (s_B = s_val = 2).
+        B16 = B.half()
+        run16 = lambda: ra_spmm.run_tile_plan_route(plan, B16, "fp16")  # noqa: E731
+        w16, e16 = timed_steps(run16, steps, warmup)
+        b16 = bytes_alg(g.M, g.K, g.nnz, N, s_val=2, s_b=2)
+        res["native_fp16_B"] = {
+            "ms_per_step": w16, "event_ms_per_step": e16, "gflops": flops / (w16 * 1e-3) / 1e9,
+            "bytes_alg": b16, "roofline_frac": b16 / (e16 * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "identical_to_fp32_B_call": bool(torch.equal(run16(), C)),
+        }
+        log(f"[bench] native fp16 B: {w16:.4f} ms/step, {res['native_fp16_B']['gflops']:.1f} GFLOP/s, "
+            f"identical to the fp32-B call: {res['native_fp16_B']['identical_to_fp32_B_call']}")
+        del B16
     if do_cpu:
         port, ts = cpu_baselines(g, N)
         res["cpu_port"] = port
@@ -360,6 +376,19 @@ def sweep(configs, Ns, steps, out_path):
                 rows.append(row)
                 log(f"[sweep] {cfg} N={N:4d} {label:22s} {wall:9.3f} ms {row['gflops']:9.1f} GF/s "
                     f"build {build:8.1f} ms err {err:.2e}")
+                if label in ("TC_DIRECT", "COMMUNITY_TC", "SEGMENT_HYBRID") and cfg in ("C3", "C4") \
+                        and N % 8 == 0:
+                    # fp16-B configs: the native 16-bit-B entry, no conversion pass
+                    B16 = B.half()
+                    f16 = lambda: ra_spmm.run_tile_plan_route(plan, B16, "fp16")  # noqa: E731
+                    w16, e16 = timed_steps(f16, steps, 3)
+                    err16 = float(((f16() - base).abs() / (scale + 1e-30)).max())
+                    rows.append({"config": cfg, "N": N, "path": label + "+B16", "ms": w16, "event_ms": e16,
+                                 "gflops": 2.0 * g.nnz * N / (w16 * 1e-3) / 1e9, "build_ms": build,
+                                 "max_rel_err_vs_baseline": err16, "routed": False})
+                    log(f"[sweep] {cfg} N={N:4d} {label + '+B16':22s} {w16:9.3f} ms "
+                        f"{rows[-1]['gflops']:9.1f} GF/s err {err16:.2e}")
+                    del B16
                 del plan
             del B
         del rp, ci, vl, host
@@ -455,6 +484,8 @@ def main(argv=None):
         "max_rel_err_vs_baseline": res["max_rel_err_vs_baseline"],
         "cpu_torch_sparse": res.get("cpu_torch_sparse"),
     }
+    if "native_fp16_B" in res:
+        line["native_fp16_B"] = res["native_fp16_B"]
     if args.details:
         Path(args.details).parent.mkdir(parents=True, exist_ok=True)
         Path(args.details).write_text(json.dumps(res, indent=1))
