@@ -201,12 +201,12 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_kernel(
             a = a_half ? apair : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         } else {
             // The partner's register holds this step's row of block b+q.
-            const u32x4 w = __builtin_bit_cast(u32x4, apair);
+            const u32x4 mine = __builtin_bit_cast(u32x4, apair);
             u32x4 o;
-            o[0] = __shfl_xor(w[0], 8, kWave);
-            o[1] = __shfl_xor(w[1], 8, kWave);
-            o[2] = __shfl_xor(w[2], 8, kWave);
-            o[3] = __shfl_xor(w[3], 8, kWave);
+            o[0] = __shfl_xor(mine[0], 8, kWave);
+            o[1] = __shfl_xor(mine[1], 8, kWave);
+            o[2] = __shfl_xor(mine[2], 8, kWave);
+            o[3] = __shfl_xor(mine[3], 8, kWave);
             a = a_half ? __builtin_bit_cast(u16x8, o) : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         }
         Run raw[8];
