@@ -11,7 +11,6 @@ import csv
 from pathlib import Path
 
 import numpy as np
-import pytest
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "router_golden.csv"
 

@@ -7,7 +7,6 @@ closed forms B = ones (row sums) and B = unit columns (columns of A), and (d)
 empty rows -> zero rows.
 """
 import numpy as np
-import pytest
 import scipy.sparse as sp
 
 from ra_spmm import synthetic as S
