@@ -93,3 +93,22 @@ def test_c3_device_build_matches_host():
     g = S.CONFIGS["C3"]()
     for kind in (0, 1):
         _compare(g, kind, "fp16", 256)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_device_build_matches_host_random(seed):
+    """Seeded shapes, densities, skew, empty rows and duplicates: the device
+    build equals the host build array for array."""
+    rng = np.random.default_rng(500 + seed)
+    M, K = int(rng.integers(1, 2500)), int(rng.integers(1, 4000))
+    d = float(rng.choice([1.0, 6.0, 30.0, 120.0]))
+    g = S.random_csr(M, K, min(d, K), seed=int(rng.integers(1 << 30)), skew=float(rng.choice([0.0, 1.1])),
+                     empty_frac=float(rng.choice([0.0, 0.2])), max_deg=K)
+    if rng.random() < 0.4 and g.nnz > 1:  # repeated (row, column) entries
+        ci = g.colind.copy()
+        ci[1::3] = ci[0:-1:3][: len(ci[1::3])]
+        g = S.Graph(g.rowptr, ci, g.vals, M, K, "dups")
+    kind = int(rng.integers(0, 3))
+    value_dtype = "bf16" if rng.random() < 0.3 else "fp16"
+    print(f"[tile-build] random seed={seed} M={M} K={K} nnz={g.nnz} kind={kind} {value_dtype}", flush=True)
+    _compare(g, kind, value_dtype, N=int(rng.choice([16, 64, 200])))
