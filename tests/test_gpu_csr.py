@@ -176,7 +176,10 @@ ZO_INFO = ("M", "K", "num_tiny", "num_short", "num_medium", "num_long", "num_emp
 ZO_LISTS = ("short_rows", "chunk_rows", "chunk_starts", "chunk_slot", "split_rows", "split_off")
 
 
-@pytest.mark.parametrize("case", ["hubs", "all_empty", "all_long", "one_row", "mixed_large"])
+RANDOM_ZO = [f"random{i}" for i in range(12)]
+
+
+@pytest.mark.parametrize("case", ["hubs", "all_empty", "all_long", "one_row", "mixed_large"] + RANDOM_ZO)
 def test_zero_overhead_device_binning_matches_host_and_oracle(oracle, case):
     """Device binning (one scan on the GPU) == host binning, list for list, and
     both agree with the oracle's bins (csr/ra_zero_overhead.cu:331-358)."""
@@ -189,6 +192,13 @@ def test_zero_overhead_device_binning_matches_host_and_oracle(oracle, case):
         g = S.random_csr(40, 5000, 700.0, seed=2)
     elif case == "one_row":
         g = S.random_csr(1, 2000, 1000.0, seed=3)
+    elif case.startswith("random"):
+        # seeded degree mixes around the bin edges (4 / 16 / 64 / 256-nnz chunks)
+        rng = np.random.default_rng(700 + int(case[6:]))
+        M, K = int(rng.integers(1, 20000)), int(rng.integers(1, 30000))
+        d = float(rng.choice([2.0, 10.0, 40.0, 300.0]))
+        g = S.random_csr(M, K, min(d, K), seed=int(rng.integers(1 << 30)), skew=float(rng.choice([0.0, 1.0, 1.4])),
+                         empty_frac=float(rng.choice([0.0, 0.3])), max_deg=K)
     else:
         g = S.random_csr(200000, 50000, 6.0, seed=4, skew=1.0, empty_frac=0.1, max_deg=20000)
     rp = torch.from_numpy(g.rowptr)
