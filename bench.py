@@ -116,9 +116,16 @@ def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
     elif label == "CSR_DIRECT":
         fn = lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B)  # noqa: E731
         name = "csr_rows_kernel"
+    elif not label.endswith("_TF32") and B.shape[1] % 8 == 0:
+        # The MFMA launches alone: the same plan on B already in 16-bit, so
+        # the per-call conversion pass is left out (its bytes are not the
+        # kernel's).  Column partitions make this one launch per range.
+        Bh = B.half()  # build_kernel_plan stores fp16 values
+        fn = lambda: ra_spmm.run_tile_plan_route(plan, Bh, "fp16")  # noqa: E731
+        name = "tile_mfma_tall_kernel" if plan.rows_per_window in (16, 32) else "tile_mfma_kernel"
     else:
         fn = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
-        name = "tile kernels (path total)"
+        name = "tile path (total)"
     _, ev = timed_steps(fn, steps, 5)
     return ev, name
 
@@ -215,7 +222,8 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
     flops = 2.0 * g.nnz * N
     gflops = flops / (wall_ms * 1e-3) / 1e9
     k_ms, k_name = kernel_time_ms(label, plan, rp, ci, vl, B, steps)
-    b_alg = bytes_alg(g.M, g.K, g.nnz, N)
+    # the MFMA kernels read 16-bit B and stored values
+    b_alg = bytes_alg(g.M, g.K, g.nnz, N, *((2, 2) if k_name.startswith("tile_mfma") else (4, 4)))
 
     # Comparators on the same inputs.
     base_wall, base_ev = timed_steps(lambda: ra_spmm.spmm_csr_baseline(rp, ci, vl, B), max(20, steps // 4), 5)
