@@ -12,6 +12,7 @@ exact products; bars:
   CSR_DIRECT, baseline, fp16 guardrail   bit-identical to the oracle's fma chain
   ZERO_OVERHEAD_CSR                      rows <= 64 nnz bit-identical, all within 1e-5 of |A||B|
   tile FP16 and FP32 routes              within 1e-5 of |A||B| of the fp64 value
+  bf16 plan on bf16 B (16-bit entry)     within 1e-5 of |A||Bq| of the fp64 value on bf16-rounded B
 """
 import numpy as np
 import pytest
@@ -103,6 +104,19 @@ def test_csr_family_64bit(oracle, big):
     np.testing.assert_array_equal(C[deg <= 64], seq[deg <= 64])
     assert_close_scaled(C, oracle.spmm_f64(srp, sci, svl, Bu), oracle.spmm_f64(srp, sci, np.abs(svl), np.abs(Bu)),
                         1e-5, "zo")
+
+
+def test_bf16_tile_plan_64bit(oracle, big):
+    """bf16 values and bf16 B on the 16-bit entry (values k/64 are exact in
+    bf16; B is rounded to bf16, and the reference uses the same rounding)."""
+    srp, sci, svl, Bu, _ = big["sub"]
+    qb = oracle.quantize_bf16(Bu)
+    rp, ci, vl = big["host"]
+    p = ra_spmm.make_tc_direct_plan(rp, ci, vl, M, K, N, "bf16")
+    print("[large] bf16 plan, bf16 B", flush=True)
+    C = _rows(ra_spmm.run_tile_plan_route(p, big["B"].bfloat16(), "bf16"), big["sample"])
+    assert_close_scaled(C, oracle.spmm_f64(srp, sci, svl, qb), oracle.spmm_f64(srp, sci, np.abs(svl), np.abs(qb)),
+                        1e-5, "bf16")
 
 
 @pytest.mark.parametrize("mk", ["make_tc_direct_plan", "make_community_tc_plan", "make_segment_hybrid_plan"])
