@@ -116,9 +116,15 @@ const char* ra_path_name(int32_t path);
 const char* ra_reject_name(int32_t code);
 
 /* -------------------------------------------------------------- features
- * The four routing inputs from rowptr alone.  Both backends reduce the exact
- * integers nnz, sum(deg^2) and max(deg) and share one finalisation, so the
- * host and device paths produce bit-identical features.
+ * The four routing inputs from rowptr alone, in the reference's two forms.
+ * ra_features_host is the two-pass form of the host path: sigma^2 =
+ * sum (d - avg)^2 / M in ascending row order.  ra_features_device is the
+ * moment form of the GPU path: var = max(0, S2/M - avg^2) from the exact
+ * integers nnz and sum(deg^2) (ra_features_from_moments).  Both return zero
+ * features when M <= 0 or K <= 0, as the reference does.  The two forms'
+ * degree_cv differ by at most one float32 ulp, and only rarely (when the
+ * exact CV lies within the moment form's cancellation error of a float32
+ * rounding boundary).
  * Reference: compute_production_router_features, router/router_features.cpp:79-111
  *            compute_production_router_features_gpu, router/router_features_cuda.cu:51-92 */
 typedef struct ra_features {
@@ -165,7 +171,8 @@ typedef struct ra_diag_features {
 ra_status ra_analyze_matrix(const int32_t* h_rowptr, const int32_t* h_colind, int32_t M, int32_t K,
                             int32_t N, ra_diag_features* out);
 
-/* Shared finalisation from exact integer moments. */
+/* Moment-form finalisation from exact integer moments (the device path's;
+ * router/router_features_cuda.cu:83-91). */
 ra_status ra_features_from_moments(int32_t M, int32_t K, int32_t N, int64_t nnz,
                                    int64_t sum_deg_sq, int32_t max_deg, int64_t empty_rows,
                                    ra_features* out);

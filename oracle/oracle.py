@@ -187,14 +187,17 @@ def degree_moments(rowptr):
     return int(nnz.value), int(s2.value), int(mx.value), int(em.value)
 
 
-def features_gpu_reference(rowptr, M: int):
+def features_gpu_reference(rowptr, M: int, K: int = 1):
     """Features as the reference GPU pass computes them
-    (router/router_features_cuda.cu:78-91): avg = S1/M, var = max(0, S2/M - avg^2),
-    cv = float(std/avg).  S1, S2 are exact here (integer sums), which is what
-    the reference's fp64 atomics give while S2 < 2^53.
-    Returns (nnz, avg64, std64, avg32, std32, cv32)."""
+    (router/router_features_cuda.cu:51-92): zero features when M <= 0 or K <= 0
+    (:57-59); avg = S1/M, var = max(0, S2/M - avg^2), cv = float(std/avg).
+    S1, S2 are exact here (integer sums), which is what the reference's fp64
+    atomics give while S2 < 2^53.
+    Returns (nnz, avg64, std64, avg32, std32, cv32).
+    Pinned by numpy's population std (tests/test_oracle_router.py) and by
+    degree sequences whose CV is known in closed form."""
     nnz, s2, _, _ = degree_moments(rowptr)
-    if M <= 0:
+    if M <= 0 or K <= 0:
         return 0, 0.0, 0.0, 0.0, 0.0, 0.0
     avg = float(nnz) / float(M)
     var = max(0.0, float(s2) / float(M) - avg * avg)
@@ -203,17 +206,27 @@ def features_gpu_reference(rowptr, M: int):
     return nnz, avg, std, float(np.float32(avg)), float(np.float32(std)), float(cv)
 
 
-def features_cpu_reference(rowptr, M: int):
+def features_cpu_reference(rowptr, M: int, K: int = 1):
     """Two-pass features of compute_production_router_features
-    (router/router_features.cpp:79-111): avg = nnz/M; sigma^2 = sum (d-avg)^2 / M.
-    Returns (nnz, avg32, std32, cv32)."""
+    (router/router_features.cpp:79-111): zero features when M <= 0 or K <= 0
+    (:86-88); avg = nnz/M; when nnz <= 0 only avg is set (:94-96); otherwise
+    sigma^2 = sum_row (d - avg)^2 / M, summed in ascending row order (the
+    reference's serial loop; above 131072 rows it is an OpenMP reduction
+    whose order depends on the thread count), cv = float(sigma/avg).
+    np.cumsum adds strictly left to right, so the last element is the serial
+    double sum.  Returns (nnz, avg32, std32, cv32).
+    Pinned by numpy's population std and by degree sequences whose CV is
+    known in closed form (tests/test_oracle_router.py)."""
     rowptr = np.asarray(rowptr, dtype=np.int64)
+    if M <= 0 or K <= 0:
+        return 0, 0.0, 0.0, 0.0
     nnz = int(rowptr[M] - rowptr[0])
     avg = nnz / M
     if nnz <= 0:
         return nnz, float(np.float32(avg)), 0.0, 0.0
     deg = np.diff(rowptr[: M + 1]).astype(np.float64)
-    sq = float(np.sum((deg - avg) ** 2))
+    delta = deg - avg
+    sq = float(np.cumsum(delta * delta)[-1])
     std = math.sqrt(sq / M)
     cv = float(np.float32(std / avg)) if avg > 1e-6 else 0.0
     return nnz, float(np.float32(avg)), float(np.float32(std)), cv

@@ -9,13 +9,14 @@
 //   baseline           regime-free reference point: one wave per row, lanes
 //                      stride over columns, scalar loads.
 //   ZERO_OVERHEAD_CSR  one fused launch: hub chunks (256 nnz) first, then the
-//                      degree-binned short rows; chunks of rows longer than 256
-//                      write fp32 partials that a second launch sums in
-//                      ascending chunk order (deterministic, no atomics).
+//                      degree-binned short rows; rows of up to 256 nonzeros
+//                      keep one fma chain per element; chunks of rows longer
+//                      than 256 write fp32 partials that a second launch sums
+//                      in ascending chunk order (deterministic, no atomics).
 //   features           exact integer degree moments (nnz, sum d^2, max d,
 //                      empty rows) in two deterministic launches.
 //
-// Every output element of CSR_DIRECT, of the baseline and of short ZO rows is
+// Every output element of CSR_DIRECT, of the baseline and of ZO rows <= 256 is
 // one fp32 accumulator updated by fma in CSR order, which is bit-identical to
 // the reference per-lane accumulation (csr/csr_direct.cu:201-228).
 #include <algorithm>
@@ -196,9 +197,12 @@ __global__ __launch_bounds__(kBlock) void csr_baseline_kernel(
 }
 
 // ---------------------------------------------------------- ZERO_OVERHEAD_CSR
-// Waves [0, num_chunks) take one 256-nnz chunk each; the 64/G lane groups of
-// the wave split the chunk into contiguous parts and are summed in group order
-// through LDS.  Later waves take 64/G rows of the short-row list each.
+// Waves [0, num_chunks) take one 256-nnz chunk each.  A sole chunk (a row of
+// 65..256 nonzeros) is run by lane group 0 alone, one fma chain per element.
+// A chunk of a longer row is split by the 64/G lane groups of the wave into
+// contiguous parts that are summed in group order through LDS (with
+// RA_ZO_SOLE_SPLIT=1 sole chunks are split the same way; measured no faster
+// on C2 and C5).  Later waves take 64/G rows of the short-row list each.
 template <int G, int V, int U, typename P>
 __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
     const int32_t* __restrict__ chunk_rows, const int32_t* __restrict__ chunk_starts,
     const int32_t* __restrict__ chunk_slot, int num_chunks, P* __restrict__ partials,
     const int32_t* __restrict__ short_rows, int64_t num_short, int64_t ldp, int np, int remap,
-    int nt) {
+    int nt, int sole_split) {
     constexpr int RPW = kWave / G;
     __shared__ P red[kWavesPerBlock][(RPW > 1 ? RPW - 1 : 1) * G * V];
     const int lane = threadIdx.x & (kWave - 1);
@@ -230,6 +234,17 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
         const int row = static_cast<int>(tag & ~kSoleFlag);
         const int cs = chunk_starts[gw];
         const int ce = min(cs + kChunk, rowptr[row + 1]);
+        if ((tag & kSoleFlag) && !sole_split) {
+            // A sole chunk (a row of 65..256 nonzeros) is one lane group's
+            // single fma chain per element, as for the short rows: the same
+            // bits as CSR_DIRECT (csr/ra_zero_overhead.cu:246-262).
+            if (sub != 0) return;
+            accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, cs, ce, sl, q, acc, nt != 0);
+#pragma unroll
+            for (int s = 0; s < V; ++s)
+                if (q[s] >= 0) store_once(Cp + (int64_t)row * ldp + q[s], acc[s], nt != 0);
+            return;
+        }
         constexpr int L = kChunk / RPW;
         const int a = min(cs + sub * L, ce);
         const int b = min(a + L, ce);
@@ -407,10 +422,12 @@ struct LaneShape {
 // (RA_ZO_XCD_REMAP=1 turns it on for ZERO_OVERHEAD_CSR, where it piles the hub
 // chunks onto one XCD), RA_CSR_STREAMING=0 turns the non-temporal hints off,
 // RA_CSR_COLTILE=c processes the columns in passes of c elements (the grid's
-// slowest dimension), so each pass gathers only a c-column slice of B.
+// slowest dimension), so each pass gathers only a c-column slice of B;
+// RA_ZO_SOLE_SPLIT=1 splits sole ZO chunks over the wave's lane groups.
 struct CsrTuning {
-    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0;
+    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0, sole_split = 0;
     CsrTuning() {
+        if (const char* e = std::getenv("RA_ZO_SOLE_SPLIT")) sole_split = std::atoi(e) != 0;
         if (const char* e = std::getenv("RA_CSR_COLTILE")) coltile = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_LANES")) lanes = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_UNROLL")) unroll = std::atoi(e) >= 8 ? 8 : 4;
@@ -471,12 +488,12 @@ ra_status launch_zo(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_
                     const int32_t* chunk_rows, const int32_t* chunk_starts,
                     const int32_t* chunk_slot, int num_chunks, P* partials,
                     const int32_t* short_rows, int64_t num_short, int64_t ldp, int np) {
-    const int remap = tuning().zo_remap, nt = tuning().nt;
+    const int remap = tuning().zo_remap, nt = tuning().nt, sole_split = tuning().sole_split;
 #define RA_ZO_CASE(g, v, u)                                                                  \
     if (sh.G == g && sh.V == v && sh.U == u) {                                               \
         zo_fused_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(                                \
             rowptr, colind, vals, B, C, chunk_rows, chunk_starts, chunk_slot, num_chunks,    \
-            partials, short_rows, num_short, ldp, np, remap, nt);                            \
+            partials, short_rows, num_short, ldp, np, remap, nt, sole_split);                \
         RA_LAUNCH_CHECK("zo_fused_kernel");                                                  \
         return RA_OK;                                                                        \
     }

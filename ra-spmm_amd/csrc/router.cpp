@@ -117,11 +117,12 @@ ra_status ra_features_from_moments(int32_t M, int32_t K, int32_t N, int64_t nnz,
     out->M = M;
     out->K = K;
     out->N = N;
+    // No features for an empty shape (router/router_features_cuda.cu:57-59).
+    if (M <= 0 || K <= 0) return RA_OK;
     out->nnz = nnz;
     out->sum_deg_sq = sum_deg_sq;
     out->max_deg = max_deg;
     out->empty_rows = empty_rows;
-    if (M <= 0) return RA_OK;
     // Moment form of router/router_features_cuda.cu:83-91 on exact integers.
     const double avg = static_cast<double>(nnz) / static_cast<double>(M);
     double var = static_cast<double>(sum_deg_sq) / static_cast<double>(M) - avg * avg;
@@ -138,8 +139,17 @@ ra_status ra_features_from_moments(int32_t M, int32_t K, int32_t N, int64_t nnz,
 
 ra_status ra_features_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_t N,
                            ra_features* out) {
+    if (!out) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: out is NULL");
     if (!h_rowptr && M > 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: rowptr is NULL");
     if (M < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "features: M < 0");
+    std::memset(out, 0, sizeof(*out));
+    out->M = M;
+    out->K = K;
+    out->N = N;
+    // Two-pass form of router/router_features.cpp:79-111: no features for an
+    // empty shape (:86-88); avg only when nnz <= 0 (:94-96); otherwise
+    // sigma^2 = sum (d - avg)^2 / M, summed in ascending row order.
+    if (M == 0 || K <= 0) return RA_OK;
     int64_t s2 = 0, empty = 0;
     int32_t mx = 0;
     for (int32_t r = 0; r < M; ++r) {
@@ -149,8 +159,26 @@ ra_status ra_features_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_
         if (d > mx) mx = static_cast<int32_t>(d);
         empty += (d == 0);
     }
-    const int64_t nnz = M > 0 ? static_cast<int64_t>(h_rowptr[M]) - h_rowptr[0] : 0;
-    return ra_features_from_moments(M, K, N, nnz, s2, mx, empty, out);
+    const int64_t nnz = static_cast<int64_t>(h_rowptr[M]) - h_rowptr[0];
+    out->nnz = nnz;
+    out->sum_deg_sq = s2;
+    out->max_deg = mx;
+    out->empty_rows = empty;
+    const double avg = static_cast<double>(nnz) / static_cast<double>(M);
+    out->avg = avg;
+    out->avg_nnz_per_row = static_cast<float>(avg);
+    if (nnz <= 0) return RA_OK;
+    double dev2 = 0.0;
+    for (int32_t r = 0; r < M; ++r) {
+        const double delta = static_cast<double>(h_rowptr[r + 1] - h_rowptr[r]) - avg;
+        dev2 += delta * delta;
+    }
+    const double std_dev = std::sqrt(dev2 / static_cast<double>(M));
+    out->std_dev = std_dev;
+    out->std_nnz_per_row = static_cast<float>(std_dev);
+    out->degree_cv = (avg > 1e-6) ? static_cast<float>(std_dev / avg) : 0.0f;
+    out->max_to_mean_ratio = (avg > 1e-6) ? static_cast<float>(mx / avg) : 0.0f;
+    return RA_OK;
 }
 
 ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t table,

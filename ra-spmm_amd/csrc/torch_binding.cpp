@@ -173,7 +173,7 @@ ra_features features_of(const torch::Tensor& rowptr, int M, int K, int N, const 
     } else {
         auto rp = host_i32(rowptr);
         check(ra_features_host(rp.data_ptr<int32_t>(), M, K, N, &f), "features");
-        *backend = "cpu_rowptr_moments";
+        *backend = "cpu_rowptr";  // bindings/ra_bindings.cpp:1726
     }
     return f;
 }

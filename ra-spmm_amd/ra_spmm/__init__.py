@@ -35,7 +35,8 @@ from .dispatch import (  # noqa: F401
     spmm_cusparse_fp16,
 )
 from .router import (  # noqa: F401
-    MI355X, REFERENCE, RouterTable, features_from_moments, production_features, route_label,
+    MI355X, REFERENCE, RouterTable, features_from_moments, features_two_pass, production_features,
+    route_label,
     route_with_rules, simple_router,
 )
 

@@ -38,32 +38,53 @@ _FIXED = {"csr_direct": "CSR_DIRECT", "zero_overhead": "ZERO_OVERHEAD_CSR",
           "community_tc": "COMMUNITY_TC", "segment_hybrid": "SEGMENT_HYBRID"}
 
 
+_AGGREGATIONS = ("gcn", "sage", "graphsage", "gin")
+
+
 def build_aggregation_operator(csr, model: str):
-    """Per-model aggregation matrix (scipy CSR, fp32, sorted indices):
-    GCN  D~^-1/2 (A + I) D~^-1/2 (self-loop added only where absent),
-    SAGE D^-1 A (zero-degree rows stay zero), GIN A unchanged."""
+    """Aggregation matrix of a GNN layer as scipy CSR (fp32, sorted columns).
+
+    gcn           W[i, j] = a~_ij / sqrt(deg~_i * deg~_j), where a~ is A with a
+                  unit self-loop on every row whose diagonal entry is zero or
+                  absent, and deg~ its row sums (rows of zero degree stay 0)
+    sage          W[i, j] = a_ij / deg_i (row mean; empty rows stay zero)
+    gin           W = A
+    Duplicate entries of A are summed first.  The matrix is built once, so
+    every backend and the correctness reference consume the same operator
+    (gnn_bench/router_vs_baselines_gcn.py:89-126)."""
     import scipy.sparse as sp
-    A = csr.tocsr().astype(np.float64)
-    A.sum_duplicates()
-    m = model.lower()
-    if m == "gin":
-        out = A.copy()
-    elif m in ("graphsage", "sage"):
-        deg = np.asarray(A.sum(axis=1)).ravel()
-        dinv = np.divide(1.0, deg, out=np.zeros_like(deg), where=deg > 0)
-        out = sp.diags(dinv) @ A
-    elif m == "gcn":
-        eye = sp.eye(A.shape[0], format="csr", dtype=np.float64)
-        eye.data[A.diagonal() != 0] = 0.0
-        Ahat = (A + eye).tocsr()
-        Ahat.eliminate_zeros()
-        d = np.asarray(Ahat.sum(axis=1)).ravel()
-        dis = np.divide(1.0, np.sqrt(d), out=np.zeros_like(d), where=d > 0)
-        D = sp.diags(dis)
-        out = D @ Ahat @ D
+    kind = model.lower()
+    if kind not in _AGGREGATIONS:
+        raise ValueError(f"no aggregation operator for model {model!r} "
+                         f"(expected one of {', '.join(_AGGREGATIONS)})")
+    adj = sp.csr_matrix(csr, dtype=np.float64, copy=True)
+    adj.sum_duplicates()
+    n = adj.shape[0]
+
+    def row_of_entry(m):
+        return np.repeat(np.arange(m.shape[0]), np.diff(m.indptr))
+
+    def reciprocal(x, power):
+        r = np.zeros_like(x)
+        live = x > 0
+        r[live] = x[live] ** -power
+        return r
+
+    if kind == "gcn":
+        missing_loop = (adj.diagonal() == 0).astype(np.float64)
+        tilde = (adj + sp.diags(missing_loop, format="csr")).tocsr()
+        tilde.eliminate_zeros()
+        tilde.sort_indices()
+        norm = reciprocal(np.asarray(tilde.sum(axis=1)).ravel(), 0.5)
+        tilde.data = tilde.data * (norm[row_of_entry(tilde)] * norm[tilde.indices])
+        weights = tilde
+    elif kind == "gin":
+        weights = adj
     else:
-        raise ValueError(f"unknown model for aggregation operator: {model}")
-    out = out.tocsr().astype(np.float32)
+        inv_deg = reciprocal(np.asarray(adj.sum(axis=1)).ravel(), 1.0)
+        weights = adj.copy()
+        weights.data = weights.data * inv_deg[row_of_entry(weights)]
+    out = sp.csr_matrix(weights, dtype=np.float32)
     out.sort_indices()
     return out
 
@@ -198,8 +219,9 @@ def validate_backend(csr, device, backend: str, ncols_values, seed: int, table="
         deg = t["rowptr_cpu"][1:] - t["rowptr_cpu"][:-1]
         max_row = max(1, int(deg.max().item())) if deg.numel() else 1
         for ncols in sorted(set(int(v) for v in ncols_values)):
-            torch.manual_seed(seed + ncols + int(transpose))
-            B = torch.randn((csr.shape[0], ncols), device=device)
+            gen = torch.Generator(device=device).manual_seed(
+                (int(seed) * 8191 + ncols) * 2 + int(transpose))
+            B = torch.randn((csr.shape[0], ncols), device=device, generator=gen)
             out = graph.run(B, backend, transpose)
             ref = _C.spmm_cusparse(t["rowptr"], t["colind"], t["vals"], B)
             err = float((out.float() - ref).abs().max().item())

@@ -4,9 +4,10 @@ Reference: route_with_rules / simple_router, ra_router_eval.py:37-129, and the
 C++ deployed block router/router_dispatch.cpp:979-1110.
 
 Bit-identity with the C++ router is by construction:
-  * features come from exact integer moments (nnz, sum of squared row lengths)
-    with the same IEEE-754 double operations as ra_features_from_moments, then
-    rounded to float32 (``production_features``);
+  * the decision reads float32 features; ``production_features`` reproduces
+    both feature forms of the C++ side bit for bit (the moment form of the
+    device pass, ra_features_from_moments, and the two-pass form of the host
+    pass, ra_features_host);
   * every comparison is float32 value vs float32 threshold, evaluated on the
     exactly representable doubles (``_f32``), which is what the C++ float
     comparisons compute;
@@ -25,7 +26,7 @@ import numpy as np
 
 __all__ = [
     "RouterTable", "REFERENCE", "MI355X", "TABLES", "production_features",
-    "features_from_moments", "route_with_rules", "simple_router", "route_label",
+    "features_from_moments", "features_two_pass", "route_with_rules", "simple_router", "route_label",
 ]
 
 
@@ -76,9 +77,10 @@ MI355X = RouterTable(plan_s_per_nnz=1e-9, fp32_route_csr=True, skewed_to_zo=Fals
 TABLES = {"reference": REFERENCE, "mi355x": MI355X}
 
 
-def features_from_moments(M: int, nnz: int, sum_deg_sq: int):
-    """(d32, cv32) exactly as ra_features_from_moments computes them."""
-    if M <= 0:
+def features_from_moments(M: int, nnz: int, sum_deg_sq: int, K: int = 1):
+    """(d32, cv32) exactly as ra_features_from_moments computes them (the
+    device form, router/router_features_cuda.cu:83-91)."""
+    if M <= 0 or K <= 0:
         return 0.0, 0.0
     avg = float(nnz) / float(M)
     var = float(sum_deg_sq) / float(M) - avg * avg
@@ -90,18 +92,44 @@ def features_from_moments(M: int, nnz: int, sum_deg_sq: int):
     return d32, cv32
 
 
-def production_features(rowptr, M: int | None = None):
-    """Canonical routing features of a CSR rowptr (numpy / torch / list).
+def features_two_pass(rowptr, M: int, K: int = 1):
+    """(d32, cv32) exactly as ra_features_host computes them (the host form,
+    router/router_features.cpp:79-111): sum (d - avg)^2 in ascending row
+    order (np.cumsum adds left to right)."""
+    rp = np.asarray(rowptr.cpu() if hasattr(rowptr, "cpu") else rowptr, dtype=np.int64)
+    if M <= 0 or K <= 0:
+        return 0.0, 0.0
+    nnz = int(rp[M] - rp[0])
+    avg = nnz / M
+    if nnz <= 0:
+        return _f32(avg), 0.0
+    delta = np.diff(rp[: M + 1]).astype(np.float64) - avg
+    std = math.sqrt(float(np.cumsum(delta * delta)[-1]) / M)
+    return _f32(avg), (_f32(std / avg) if avg > 1e-6 else 0.0)
 
+
+def production_features(rowptr, M: int | None = None, K: int | None = None,
+                        form: str = "moments"):
+    """Routing features of a CSR rowptr (numpy / torch / list).
+
+    ``form="moments"`` gives the device path's values (ra_features_device),
+    ``form="two_pass"`` the host path's (ra_features_host).
     Returns dict(M, nnz, sum_deg_sq, max_deg, avg_nnz_per_row, degree_cv).
     """
     rp = np.asarray(rowptr.cpu() if hasattr(rowptr, "cpu") else rowptr, dtype=np.int64)
     if M is None:
         M = len(rp) - 1
+    if K is None:
+        K = max(M, 1)
     deg = np.diff(rp[: M + 1])
     nnz = int(rp[M] - rp[0]) if M > 0 else 0
     s2 = int(np.dot(deg, deg)) if M > 0 else 0
-    d32, cv32 = features_from_moments(M, nnz, s2)
+    if form == "moments":
+        d32, cv32 = features_from_moments(M, nnz, s2, K)
+    elif form == "two_pass":
+        d32, cv32 = features_two_pass(rp, M, K)
+    else:
+        raise ValueError(f"unknown feature form {form!r}")
     return {"M": M, "nnz": nnz, "sum_deg_sq": s2, "max_deg": int(deg.max()) if M > 0 else 0,
             "avg_nnz_per_row": d32, "degree_cv": cv32}
 

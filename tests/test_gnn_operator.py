@@ -86,3 +86,24 @@ def test_gcn_order_argument():
     assert gnn.GCN(4, 8, 3, order="auto").order == "auto"
     with pytest.raises(ValueError):
         gnn.GCN(4, 8, 3, order="aggregate")
+
+
+def test_gcn_operator_self_loops_and_duplicates():
+    """Closed form on a matrix with an existing self-loop (kept, not doubled),
+    a duplicate entry (summed), an empty row and a stored zero diagonal
+    (treated as absent)."""
+    A = sp.csr_matrix((np.r_[2.0, 1.0, 1.0, 1.0, 1.0, 0.0, 3.0], np.r_[0, 1, 0, 2, 2, 2, 1],
+                       np.r_[0, 2, 5, 7, 7]), shape=(4, 4))  # row 1 has (1,2) twice
+    dense = A.toarray()
+    want = dense.copy()
+    for i in range(4):
+        if want[i, i] == 0:
+            want[i, i] = 1.0
+    d = want.sum(1)
+    ref = want / np.sqrt(d)[:, None] / np.sqrt(d)[None, :]
+    op = build_aggregation_operator(A, "gcn")
+    np.testing.assert_allclose(op.toarray(), ref, rtol=1e-6)
+    assert op.has_sorted_indices and op.dtype == np.float32
+    sage = build_aggregation_operator(A, "sage").toarray()
+    rs = dense.sum(1)
+    np.testing.assert_allclose(sage[rs > 0], (dense / np.where(rs > 0, rs, 1)[:, None])[rs > 0], rtol=1e-6)

@@ -41,7 +41,7 @@ def test_route_and_zero_overhead_through_the_abi(oracle):
     capi.check(lib.ra_zo_plan_run(plan, P(rp), P(ci), P(vl), P(Bd), P(C), 128, _stream()))
     torch.cuda.synchronize()
     lib.ra_zo_plan_destroy(plan)
-    short = np.diff(g.rowptr) <= 64
+    short = np.diff(g.rowptr) <= 256
     seq = oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
     np.testing.assert_array_equal(C.cpu().numpy()[short], seq[short])
     assert_close_scaled(C.cpu().numpy(), oracle.spmm_f64(g.rowptr, g.colind, g.vals, B),

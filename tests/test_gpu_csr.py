@@ -1,11 +1,12 @@
-"""GPU parity of the CSR family (CSR_DIRECT, baseline, ZERO_OVERHEAD_CSR) and
-the GPU feature pass, against the oracle.
+"""GPU parity of the CSR family (CSR_DIRECT, baseline, ZERO_OVERHEAD_CSR)
+against the oracle (the feature pass: test_gpu_features.py).
 
-Bar: CSR_DIRECT, the baseline kernel and the short-row bins (<= 64 nnz) of
-ZERO_OVERHEAD_CSR are bit-identical to oracle.spmm_seq_f32 (same fma chain per
-element).  Rows longer than 64 nnz go through 256-nnz chunks whose parts are
-summed in a fixed order: within 1e-5 of |A||B| (elementwise) of the fp64
-value, and bit-identical from run to run.
+Bar: CSR_DIRECT, the baseline kernel and the rows of ZERO_OVERHEAD_CSR with
+<= 256 nnz (the short-row bins and the sole chunks) are bit-identical to
+oracle.spmm_seq_f32 (same fma chain per element).  Rows longer than 256 nnz
+are split into 256-nnz chunks whose parts are summed in a fixed order: within
+1e-5 of |A||B| (elementwise) of the fp64 value, and bit-identical from run to
+run.
 """
 import numpy as np
 import pytest
@@ -87,7 +88,7 @@ def test_zero_overhead_hub_rows(oracle, N):
         bins["num_tiny"], bins["num_short"], bins["num_medium"], bins["num_long"], bins["num_empty"])
     C = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, torch.from_numpy(B).cuda()).cpu().numpy()
     seq = oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
-    short = deg <= 64
+    short = deg <= 256
     np.testing.assert_array_equal(C[short], seq[short])
     c64 = oracle.spmm_f64(g.rowptr, g.colind, g.vals, B)
     scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B))
@@ -95,19 +96,6 @@ def test_zero_overhead_hub_rows(oracle, N):
     # Deterministic: a second run is bit-identical.
     C2 = ra_spmm.run_zero_overhead_plan(plan, rp, ci, vl, torch.from_numpy(B).cuda()).cpu().numpy()
     np.testing.assert_array_equal(C, C2)
-
-
-def test_features_device_equals_host():
-    for seed, (M, d, skew) in enumerate([(1, 3.0, 0), (1000, 5.0, 1.0), (200_003, 12.0, 1.1)]):
-        g = S.random_csr(M, 5000, d, seed=seed, skew=skew, empty_frac=0.01)
-        rp = torch.from_numpy(g.rowptr)
-        fd = ra_spmm.compute_features(rp.cuda(), M, 5000, 64)
-        fh = ra_spmm.compute_features(rp, M, 5000, 64)
-        for k in ("nnz", "sum_deg_sq", "max_deg", "empty_rows", "avg_nnz_per_row", "degree_cv"):
-            assert fd[k] == fh[k], k
-        py = ra_spmm.production_features(g.rowptr)
-        assert fd["avg_nnz_per_row"] == py["avg_nnz_per_row"]
-        assert fd["degree_cv"] == py["degree_cv"]
 
 
 def test_router_plan_device_equals_host():
@@ -241,7 +229,7 @@ def test_c5_full_size_routed_widths(oracle):
     sub_rp = np.concatenate([[0], np.cumsum(deg[rows])]).astype(np.int32)
     sub_ci = np.concatenate([g.colind[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
     sub_vl = np.concatenate([g.vals[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
-    short = deg[rows] <= 64
+    short = deg[rows] <= 256
     for N in (256, 48):
         print(f"[c5 full] N={N}", flush=True)
         plan_dict = ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N)

@@ -127,8 +127,8 @@ def test_zero_overhead_plan_shared_across_widths():
 def test_padded_narrow_width_is_exact(oracle):
     """Widths not divisible by 4 run on a zero-padded copy in the CSR family.
     CSR_DIRECT keeps its fma chain per element: bit-identical to the unpadded
-    call.  ZERO_OVERHEAD_CSR's chunked rows (> 64 nnz) split a chunk over lane
-    groups whose count depends on the width, so only rows <= 64 nnz are
+    call.  ZERO_OVERHEAD_CSR's split rows (> 256 nnz) divide a chunk over lane
+    groups whose count depends on the width, so only rows <= 256 nnz are
     bit-identical; the rest stay within 1e-5 of |A||B|."""
     g = S.random_csr(3000, 3000, 12.0, seed=11, skew=1.0)
     import scipy.sparse as sp
@@ -143,7 +143,7 @@ def test_padded_narrow_width_is_exact(oracle):
     p = ra_spmm.make_zero_overhead_plan(t["rowptr"], g.M, g.K)
     got = graph.run(B, "zero_overhead").cpu().numpy()
     ref = ra_spmm.run_zero_overhead_plan(p, t["rowptr"], t["colind"], t["vals"], B).cpu().numpy()
-    short = np.diff(g.rowptr) <= 64
+    short = np.diff(g.rowptr) <= 256
     np.testing.assert_array_equal(got[short], ref[short])
     scale = oracle.spmm_f64(g.rowptr, g.colind, np.abs(g.vals), np.abs(B.cpu().numpy()))
     assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-30)

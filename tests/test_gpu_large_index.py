@@ -10,7 +10,7 @@ the oracle on the sub-matrix of those rows and the B rows they touch.
 Values and B are exactly representable in fp16, so the tile routes compute
 exact products; bars:
   CSR_DIRECT, baseline, fp16 guardrail   bit-identical to the oracle's fma chain
-  ZERO_OVERHEAD_CSR                      rows <= 64 nnz bit-identical, all within 1e-5 of |A||B|
+  ZERO_OVERHEAD_CSR                      rows <= 256 nnz bit-identical, all within 1e-5 of |A||B|
   tile FP16 and FP32 routes              within 1e-5 of |A||B| of the fp64 value
   bf16 plan on bf16 B (16-bit entry)     within 1e-5 of |A||Bq| of the fp64 value on bf16-rounded B
 """
@@ -101,7 +101,7 @@ def test_csr_family_64bit(oracle, big):
     print("[large] zero_overhead", flush=True)
     z = ra_spmm.make_zero_overhead_plan(rp, M, K)
     C = _rows(ra_spmm.run_zero_overhead_plan(z, rp, ci, vl, big["B"]), big["sample"])
-    np.testing.assert_array_equal(C[deg <= 64], seq[deg <= 64])
+    np.testing.assert_array_equal(C[deg <= 256], seq[deg <= 256])
     assert_close_scaled(C, oracle.spmm_f64(srp, sci, svl, Bu), oracle.spmm_f64(srp, sci, np.abs(svl), np.abs(Bu)),
                         1e-5, "zo")
 

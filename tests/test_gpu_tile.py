@@ -10,7 +10,7 @@ inflate them):
   FP32-FMA route    (replaces the reference TF32 path) every kind:
                     bit-identical to the sequential fp32 fma chain over the
                     fp16-stored values in column order; on skewed rows (CV >=
-                    1.5) rows of <= 64 stored nonzeros bit-identical and the
+                    1.5) rows of <= 256 stored nonzeros bit-identical and the
                     rest 1e-5 (conftest.assert_fp32_route).
 The reference's own gate is 1e-2 * sqrt(max row nnz) absolute for tile paths
 (ra_real_graph_eval.py:41-51, 478-495); every bound above is tighter.

@@ -69,3 +69,16 @@ def test_quantizers(oracle):
     z = np.array([1 + 2**-11, -(1 + 2**-11), 1 + 2**-12], np.float32)
     np.testing.assert_array_equal(oracle.quantize_tf32_rna(z),
                                   np.array([1 + 2**-10, -(1 + 2**-10), 1.0], np.float32))
+
+
+def test_seq_f32_equals_torch_sparse_cpu_on_c1(oracle):
+    """Config C1's stated bit-level reference is torch.sparse CPU SpMM.  On
+    this host it equals the oracle's sequential fma chain bit for bit."""
+    import torch
+    g = S.CONFIGS["C1"]()
+    for N in (64, 128):
+        B = np.random.default_rng(N).standard_normal((g.K, N)).astype(np.float32)
+        A = torch.sparse_csr_tensor(torch.from_numpy(g.rowptr).long(), torch.from_numpy(g.colind).long(),
+                                    torch.from_numpy(g.vals), (g.M, g.K))
+        ts = torch.sparse.mm(A, torch.from_numpy(B)).numpy()
+        np.testing.assert_array_equal(oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B), ts)

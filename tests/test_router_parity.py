@@ -80,7 +80,7 @@ def test_production_features_match_cpp_host_features():
     import torch
     for seed in range(3):
         g = S.random_csr(3000, 3000, 6.0 + seed, seed=seed, skew=1.1, empty_frac=0.02)
-        py = ra_spmm.production_features(g.rowptr)
+        py = ra_spmm.production_features(g.rowptr, form="two_pass")
         c = ra_spmm.compute_features(torch.from_numpy(g.rowptr), g.M, g.K, 64)
         for k in ("nnz", "sum_deg_sq", "max_deg", "avg_nnz_per_row", "degree_cv"):
             assert py[k] == c[k], k
@@ -97,7 +97,7 @@ def test_plan_dict_schema():
                 "feature_backend"):
         assert key in d, key
     assert d["path_count"] == 15 and len(d["path_names"]) == 15
-    assert d["feature_set"] == "production_4" and d["feature_backend"] == "cpu_rowptr_moments"
+    assert d["feature_set"] == "production_4" and d["feature_backend"] == "cpu_rowptr"
     assert d["rejection_codes"][d["chosen_path"]] == "CHOSEN"
     small = ra_spmm.make_router_plan(rp, rp, rp, 4, 4, 8)
     assert not small["feasible_by_path"]["TC_DIRECT"]
