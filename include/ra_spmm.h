@@ -266,6 +266,17 @@ ra_status ra_zo_plan_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_
 ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
                                const int32_t* d_colind, const float* d_vals, const float* d_B,
                                float* d_C, int32_t N, int32_t stage, ra_stream_t stream);
+/* No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same kernels and results as ra_zo_plan_run, but the partial
+ * slots of rows longer than 256 nonzeros live in a fixed 64 MiB device array
+ * of the library (one per GPU, held until the process ends) instead of a
+ * plan-owned buffer, and no call allocates.  num_split_chunks * N * 4 bytes
+ * must fit in 64 MiB, else RA_ERR_UNSUPPORTED.  Calls on one GPU share the
+ * array: calls that overlap on one GPU race. */
+ra_status ra_zo_plan_run_noalloc(ra_zo_plan* plan, const int32_t* d_rowptr,
+                                 const int32_t* d_colind, const float* d_vals, const float* d_B,
+                                 float* d_C, int32_t N, ra_stream_t stream);
 ra_status ra_zo_plan_get_info(const ra_zo_plan* plan, ra_zo_info* info);
 void ra_zo_plan_destroy(ra_zo_plan* plan);
 

@@ -551,6 +551,90 @@ ra_status csr_direct_launch(const int32_t* d_rowptr, const int32_t* d_colind, co
 
 }  // namespace ra
 
+// ------------------------------------------------ fixed scratch (no alloc)
+// ra_zo_plan_run_noalloc keeps the split rows' partial slots in this array
+// instead of a plan-owned allocation.  Every GPU the library runs on holds its
+// own copy for the life of the process; calls on one GPU share it (each call
+// writes every slot it reads, so nothing needs clearing), so calls that
+// overlap on one GPU race.  Host code never passes the array's name to a
+// kernel: it takes the device address from hipGetSymbolAddress, once per
+// device, and uses that.
+constexpr uint64_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[64] = {};
+
+static ra_status noalloc_scratch(void** out) {
+    int dev = 0;
+    RA_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return ra::fail(RA_ERR_UNSUPPORTED, "noalloc scratch: device id >= 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return ra::fail(RA_ERR_HIP, "noalloc scratch: hipGetSymbolAddress failed");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return RA_OK;
+}
+
+// partials: the split chunks' slot buffer ([num_split_chunks][N] fp32), or
+// NULL to use (and grow) the plan's own.
+static ra_status zo_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
+                 const float* d_vals, const float* d_B, float* d_C, int32_t N, int32_t stage,
+                 float* partials, hipStream_t st) {
+    if (stage < 0 || stage > 2) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: stage must be 0, 1 or 2");
+    if (!plan) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: plan is NULL");
+    const int32_t M = plan->info.M;
+    RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals, d_B, d_C, M, plan->info.K, N, 0));
+    if (M == 0 || N == 0) return RA_OK;
+    const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
+    const int np = vec ? N / 4 : N;
+    const LaneShape sh = pick_shape(np, vec ? 4 : 1);
+    if (plan->info.num_split_chunks > 0 && !partials) {
+        RA_TRY(plan->partials.ensure((size_t)plan->info.num_split_chunks * N * sizeof(float)));
+        partials = plan->partials.get<float>();
+    }
+    const int RPW = kWave / sh.G;
+    const int64_t waves = plan->info.num_chunks + (plan->num_short_total + RPW - 1) / RPW;
+    const int tiles = (np + sh.G * sh.V - 1) / (sh.G * sh.V);
+    if (waves > 0 && stage != 2) {
+        dim3 grid((waves + kWavesPerBlock - 1) / kWavesPerBlock, tiles);
+        ra_status s;
+        if (vec)
+            s = launch_zo<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
+                                  reinterpret_cast<const float4*>(d_B), reinterpret_cast<float4*>(d_C),
+                                  plan->chunk_rows, plan->chunk_starts,
+                                  plan->chunk_slot, plan->info.num_chunks,
+                                  reinterpret_cast<float4*>(partials), plan->short_rows,
+                                  plan->num_short_total, np, np);
+        else
+            s = launch_zo<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
+                                 plan->chunk_rows, plan->chunk_starts,
+                                 plan->chunk_slot, plan->info.num_chunks,
+                                 partials, plan->short_rows,
+                                 plan->num_short_total, np, np);
+        RA_TRY(s);
+    }
+    if (plan->info.num_split_rows > 0 && stage != 1) {
+        const int64_t threads = (int64_t)plan->info.num_split_rows * np;
+        const unsigned grid = static_cast<unsigned>((threads + kBlock - 1) / kBlock);
+        if (vec)
+            zo_merge_kernel<float4><<<grid, kBlock, 0, st>>>(
+                plan->split_rows, plan->split_off,
+                reinterpret_cast<float4*>(partials), reinterpret_cast<float4*>(d_C), np, np,
+                plan->info.num_split_rows);
+        else
+            zo_merge_kernel<float><<<grid, kBlock, 0, st>>>(
+                plan->split_rows, plan->split_off,
+                partials, d_C, np, np, plan->info.num_split_rows);
+        RA_LAUNCH_CHECK("zo_merge_kernel");
+    }
+    return RA_OK;
+}
+
 extern "C" {
 
 ra_status ra_spmm_csr_direct(const int32_t* d_rowptr, const int32_t* d_colind,
@@ -739,53 +823,24 @@ ra_status ra_zo_plan_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_
 ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
                                const int32_t* d_colind, const float* d_vals, const float* d_B,
                                float* d_C, int32_t N, int32_t stage, ra_stream_t stream) {
-    if (stage < 0 || stage > 2) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: stage must be 0, 1 or 2");
-    if (!plan) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo: plan is NULL");
-    const int32_t M = plan->info.M;
-    RA_TRY(check_spmm_args(d_rowptr, d_colind, d_vals, d_B, d_C, M, plan->info.K, N, 0));
-    if (M == 0 || N == 0) return RA_OK;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
-    const int np = vec ? N / 4 : N;
-    const LaneShape sh = pick_shape(np, vec ? 4 : 1);
-    if (plan->info.num_split_chunks > 0)
-        RA_TRY(plan->partials.ensure((size_t)plan->info.num_split_chunks * N * sizeof(float)));
-    const int RPW = kWave / sh.G;
-    const int64_t waves = plan->info.num_chunks + (plan->num_short_total + RPW - 1) / RPW;
-    const int tiles = (np + sh.G * sh.V - 1) / (sh.G * sh.V);
-    if (waves > 0 && stage != 2) {
-        dim3 grid((waves + kWavesPerBlock - 1) / kWavesPerBlock, tiles);
-        ra_status s;
-        if (vec)
-            s = launch_zo<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
-                                  reinterpret_cast<const float4*>(d_B), reinterpret_cast<float4*>(d_C),
-                                  plan->chunk_rows, plan->chunk_starts,
-                                  plan->chunk_slot, plan->info.num_chunks,
-                                  plan->partials.get<float4>(), plan->short_rows,
-                                  plan->num_short_total, np, np);
-        else
-            s = launch_zo<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
-                                 plan->chunk_rows, plan->chunk_starts,
-                                 plan->chunk_slot, plan->info.num_chunks,
-                                 plan->partials.get<float>(), plan->short_rows,
-                                 plan->num_short_total, np, np);
-        RA_TRY(s);
-    }
-    if (plan->info.num_split_rows > 0 && stage != 1) {
-        const int64_t threads = (int64_t)plan->info.num_split_rows * np;
-        const unsigned grid = static_cast<unsigned>((threads + kBlock - 1) / kBlock);
-        if (vec)
-            zo_merge_kernel<float4><<<grid, kBlock, 0, st>>>(
-                plan->split_rows, plan->split_off,
-                plan->partials.get<float4>(), reinterpret_cast<float4*>(d_C), np, np,
-                plan->info.num_split_rows);
-        else
-            zo_merge_kernel<float><<<grid, kBlock, 0, st>>>(
-                plan->split_rows, plan->split_off,
-                plan->partials.get<float>(), d_C, np, np, plan->info.num_split_rows);
-        RA_LAUNCH_CHECK("zo_merge_kernel");
-    }
-    return RA_OK;
+    return zo_run(plan, d_rowptr, d_colind, d_vals, d_B, d_C, N, stage, nullptr,
+                  reinterpret_cast<hipStream_t>(stream));
+}
+
+ra_status ra_zo_plan_run_noalloc(ra_zo_plan* plan, const int32_t* d_rowptr,
+                                 const int32_t* d_colind, const float* d_vals, const float* d_B,
+                                 float* d_C, int32_t N, ra_stream_t stream) {
+    if (!plan) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo noalloc: plan is NULL");
+    if (N < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo noalloc: N < 0");
+    const uint64_t need = (uint64_t)plan->info.num_split_chunks * (uint64_t)N * sizeof(float);
+    if (need > kNoAllocScratchBytes)
+        return ra::fail(RA_ERR_UNSUPPORTED,
+                        "zo noalloc: the split rows need more partial-slot memory than the "
+                        "fixed 64 MiB scratch (num_split_chunks * N * 4 bytes)");
+    float* slots = nullptr;
+    if (need > 0) RA_TRY(noalloc_scratch(reinterpret_cast<void**>(&slots)));
+    return zo_run(plan, d_rowptr, d_colind, d_vals, d_B, d_C, N, 0, slots,
+                  reinterpret_cast<hipStream_t>(stream));
 }
 
 ra_status ra_zo_plan_get_info(const ra_zo_plan* plan, ra_zo_info* info) {

@@ -23,7 +23,7 @@ EXPORTED = [
     "ra_features_host", "ra_features_device", "ra_features_from_moments", "ra_route_dispatch",
     "ra_analyze_matrix",
     "ra_spmm_csr_direct", "ra_spmm_csr_baseline", "ra_spmm_csr_baseline_f16", "ra_zo_bins_host", "ra_zo_plan_create",
-    "ra_zo_plan_create_device", "ra_zo_plan_export", "ra_zo_plan_run", "ra_zo_plan_run_stage", "ra_zo_plan_get_info", "ra_zo_plan_destroy", "ra_tile_host_build",
+    "ra_zo_plan_create_device", "ra_zo_plan_export", "ra_zo_plan_run", "ra_zo_plan_run_stage", "ra_zo_plan_run_noalloc", "ra_zo_plan_get_info", "ra_zo_plan_destroy", "ra_tile_host_build",
     "ra_tile_host_get_info", "ra_tile_host_export", "ra_tile_host_destroy",
     "ra_tile_plan_create", "ra_tile_plan_create_device", "ra_tile_plan_export",
     "ra_tile_plan_run", "ra_tile_plan_run_lowp",
@@ -145,6 +145,7 @@ def load():
         "ra_zo_plan_export": (ctypes.c_int, [P, ctypes.c_char_p, P, ctypes.POINTER(I64)]),
         "ra_zo_plan_run": (ctypes.c_int, [P, P, P, P, P, P, I32, P]),
         "ra_zo_plan_run_stage": (ctypes.c_int, [P, P, P, P, P, P, I32, I32, P]),
+        "ra_zo_plan_run_noalloc": (ctypes.c_int, [P, P, P, P, P, P, I32, P]),
         "ra_zo_plan_get_info": (ctypes.c_int, [P, ctypes.POINTER(ZOInfo)]),
         "ra_zo_plan_destroy": (None, [P]),
         "ra_tile_host_build": (ctypes.c_int, [I32, P, P, P, I32, I32, I32, I32, ctypes.POINTER(P)]),
