@@ -12,11 +12,17 @@ fp32 N(0,1) (synthetic, seeded), C = A @ B through the MI355X router.
             time from HIP events on the launch stream, against 8 TB/s
   cold      routing (GPU feature pass + decision) and plan build + first
             execution, each the mean of 10 repetitions
-  cpu       oracle/spmm_oracle.c sequential fma on one host core (kind "port")
-            and torch.sparse CSR on all host threads, same matrix
+  cpu       cpu_baseline: torch.sparse CSR on all host threads (the CPU
+            SpMM BASELINE names), full matrix; cpu_port: oracle/spmm_oracle.c
+            sequential fma on one host core
+  compare   the hand-written baseline CSR kernel and torch.sparse on the
+            device (torch-ROCm's vendor sparse library) on the same inputs
+  configs   every BASELINE config (C1..C5) at its own N and at N=128, each
+            with its path, warm time, roofline, cold costs, comparators and
+            torch.sparse CPU on a row sample; geomean speed-ups over them
 
-Other configurations: --config C1..C5 (parity-size workloads; not the driver
-line).  --sweep times every deployed path on the chosen configs (calibration).
+--config C1..C5 measures one config alone.  --sweep times every deployed path
+on the chosen configs (calibration of the router table).
 """
 from __future__ import annotations
 
@@ -69,39 +75,105 @@ def timed_steps(fn, steps, warmup):
     return wall, ev0.elapsed_time(ev1) / steps
 
 
-def cpu_baselines(g, N, seconds=12.0):
-    """Oracle sequential fma (1 core) and torch.sparse CSR (all threads)."""
+def _cpu_csr(g, rows=None):
+    """torch CPU CSR tensor of g (or of its first `rows` rows)."""
     import numpy as np
     import torch
+    M = g.M if rows is None else rows
+    rp = g.rowptr[: M + 1].astype(np.int64)
+    e = int(rp[-1])
+    return torch.sparse_csr_tensor(torch.from_numpy(rp), torch.from_numpy(g.colind[:e].astype(np.int64)),
+                                   torch.from_numpy(g.vals[:e]), size=(M, g.K)), e
+
+
+def torch_sparse_cpu(g, B_host, seconds, rows=None):
+    """torch.sparse.mm on a CPU CSR tensor (the reference's named CPU SpMM,
+    BASELINE config 1), all host threads, time-bounded repetitions."""
+    import torch
+    A, e = _cpu_csr(g, rows)
+    torch.sparse.mm(A, B_host)  # warm (thread pool, MKL handles)
+    reps, t_tot = 0, 0.0
+    while t_tot < seconds and reps < 50:
+        t0 = time.perf_counter()
+        torch.sparse.mm(A, B_host)
+        t_tot += time.perf_counter() - t0
+        reps += 1
+    N = int(B_host.shape[1])
+    what = "full matrix" if rows is None else f"first {rows} of {g.M} rows (nnz {e}), all of B"
+    return {"value": 2.0 * e * N * reps / t_tot / 1e9, "unit": "GFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "reference",
+            "threads": torch.get_num_threads(), "affinity_cores": len(os.sched_getaffinity(0)),
+            "sample": f"{what}, N={N}, {reps} repetitions in {t_tot:.2f} s: torch.sparse.mm on a CPU CSR "
+                      f"tensor (fp32), the reference's named CPU SpMM, {torch.get_num_threads()} threads"}
+
+
+def cpu_port(g, N, seconds=10.0):
+    """oracle/spmm_oracle.c sequential fma on one host core (the CPU
+    restatement of the reference's per-element chain)."""
+    import numpy as np
     from oracle import oracle as O
     O.build()
-    rng = np.random.default_rng(7)
-    B = rng.standard_normal((g.K, N)).astype(np.float32)
-    flops = 2.0 * g.nnz * N
+    B = np.random.default_rng(7).standard_normal((g.K, N)).astype(np.float32)
     reps, t_tot = 0, 0.0
     while t_tot < seconds and reps < 20:
         t0 = time.perf_counter()
         O.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
         t_tot += time.perf_counter() - t0
         reps += 1
-    port = {"value": flops * reps / t_tot / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": "port",
+    return {"value": 2.0 * g.nnz * N * reps / t_tot / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": "port",
             "sample": f"full matrix (M={g.M}, nnz={g.nnz}, N={N}) x {reps} repetitions, "
                       f"oracle/spmm_oracle.c sequential fma, 1 thread, {t_tot:.1f} s"}
-    A = torch.sparse_csr_tensor(torch.from_numpy(g.rowptr.astype(np.int64)),
-                                torch.from_numpy(g.colind.astype(np.int64)),
-                                torch.from_numpy(g.vals), size=(g.M, g.K))
-    Bt = torch.from_numpy(B)
-    torch.sparse.mm(A, Bt)  # warm
-    reps, t_tot = 0, 0.0
-    while t_tot < seconds / 2 and reps < 20:
-        t0 = time.perf_counter()
-        torch.sparse.mm(A, Bt)
-        t_tot += time.perf_counter() - t0
-        reps += 1
-    ts = {"value": flops * reps / t_tot / 1e9, "unit": "GFLOP/s",
-          "threads": torch.get_num_threads(), "affinity_cores": len(os.sched_getaffinity(0)),
-          "sample": f"full matrix x {reps} repetitions, torch.sparse.mm on a CPU CSR tensor"}
-    return port, ts
+
+
+def torch_sparse_gpu(rp, ci, vl, B, M, K, C_ref, steps):
+    """torch.sparse.mm on a device CSR tensor: torch-ROCm's vendor sparse
+    library SpMM (the counterpart of the reference's cuSPARSE guardrail).
+    Returns its ms per call and its max error relative to |A||B| against C_ref."""
+    import torch
+    try:
+        A = torch.sparse_csr_tensor(rp, ci, vl, size=(M, K))  # int32 indices, as the CSR arrives
+        fn = lambda: torch.sparse.mm(A, B)  # noqa: E731
+        C = fn()
+        torch.cuda.synchronize()
+        wall, ev = timed_steps(fn, steps, 2)
+        import ra_spmm
+        scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
+        err = float(((C - C_ref).abs() / (scale + 1e-30)).max())
+        del A, C, scale
+        return {"ms": wall, "event_ms": ev, "max_rel_err_vs_routed": err}
+    except Exception as exc:  # reported, never hides a failure of the routed path
+        return {"ms": None, "error": f"{type(exc).__name__}: {exc}"}
+
+
+def rocsparse_gpu(rp, ci, vl, B, C_ref, steps):
+    """rocSPARSE CSR SpMM (ra_spmm.vendor), every CSR algorithm timed on the
+    same inputs; the fastest is the vendor comparator."""
+    import torch
+    import ra_spmm
+    from ra_spmm import vendor
+    out = {"algs": {}}
+    scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
+    for alg in vendor.ALGS:
+        try:
+            C = torch.empty_like(C_ref)
+            v = vendor.RocsparseSpMM(rp, ci, vl, B, C, alg)
+            v.run()
+            torch.cuda.synchronize()
+            wall, ev = timed_steps(v.run, steps, 2)
+            err = float(((C - C_ref).abs() / (scale + 1e-30)).max())
+            out["algs"][alg] = {"ms": wall, "event_ms": ev, "max_rel_err_vs_routed": err}
+            v.close()
+            del C, v
+        except Exception as exc:  # an algorithm rocSPARSE rejects for this shape
+            out["algs"][alg] = {"ms": None, "error": f"{type(exc).__name__}: {exc}"}
+    ok = {a: r for a, r in out["algs"].items() if r.get("ms") and r["max_rel_err_vs_routed"] < 1e-3}
+    if ok:
+        best = min(ok, key=lambda a: ok[a]["ms"])
+        out.update({"ms": ok[best]["ms"], "alg": best})
+    else:
+        out["ms"] = None
+    del scale
+    return out
 
 
 def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
@@ -143,6 +215,22 @@ def copy_probe(nbytes=1 << 30):
     del src, dst
 
 
+def gather_probe(rows=1 << 20, width=128):
+    """One gather of known size: every row of a [rows, width] fp32 matrix read
+    once, in a random order (index_select over a permutation), and written
+    once.  Scales rocprofv3 FETCH_SIZE for 512-byte random row gathers, the
+    access pattern of the CSR kernels, as copy_probe does for streaming."""
+    import torch
+    src = torch.ones(rows, width, device="cuda")
+    perm = torch.randperm(rows, device="cuda")
+    torch.cuda.synchronize()
+    out = torch.index_select(src, 0, perm)
+    torch.cuda.synchronize()
+    log(f"[bench] gather probe: {rows * width * 4} bytes gathered + {rows * 8} index bytes read, "
+        f"{rows * width * 4} bytes written")
+    del src, perm, out
+
+
 def hbm_copy_gbs(nbytes=2 << 30, reps=10):
     """Device-to-device copy rate (bytes read + written per second, GB/s): the
     HBM bandwidth a streaming kernel reaches on this GPU, beside the 8 TB/s
@@ -163,14 +251,17 @@ def hbm_copy_gbs(nbytes=2 << 30, reps=10):
     return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
-def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=None):
+def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=None, g=None,
+                 cpu_seconds=10.0, cpu_rows=None, port=True):
     import numpy as np
     import torch
     import ra_spmm
     from ra_spmm import synthetic as S
 
     t0 = time.perf_counter()
-    g = S.CONFIGS[cfg]()
+    if g is None:
+        S.use_device_sort("cuda")
+        g = S.CONFIGS[cfg]()
     log(f"[bench] {cfg}: {g.name} M={g.M} nnz={g.nnz} generated in {time.perf_counter() - t0:.1f} s")
     rp, ci, vl = g.torch("cuda")
     gen = torch.Generator(device="cuda").manual_seed(1234)
@@ -226,8 +317,10 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
     b_alg = bytes_alg(g.M, g.K, g.nnz, N, *((2, 2) if k_name.startswith("tile_mfma") else (4, 4)))
 
     # Comparators on the same inputs.
-    base_wall, base_ev = timed_steps(lambda: ra_spmm.spmm_csr_baseline(rp, ci, vl, B), max(20, steps // 4), 5)
-    cd_wall, cd_ev = timed_steps(lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B), max(20, steps // 4), 5)
+    base_wall, base_ev = timed_steps(lambda: ra_spmm.spmm_csr_baseline(rp, ci, vl, B), max(5, steps // 4), 2)
+    cd_wall, cd_ev = timed_steps(lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B), max(5, steps // 4), 2)
+    vendor = torch_sparse_gpu(rp, ci, vl, B, g.M, g.K, C, max(3, steps // 8))
+    roc = rocsparse_gpu(rp, ci, vl, B, C, max(5, steps // 4))
     C_base = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
     scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
     max_rel = float(((C - C_base).abs() / (scale + 1e-30)).max())
@@ -247,6 +340,10 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
         "csr_direct_ms": cd_wall, "csr_direct_gflops": flops / (cd_wall * 1e-3) / 1e9,
         "speedup_vs_baseline": base_wall / wall_ms,
         "max_rel_err_vs_baseline": max_rel,
+        "torch_sparse_gpu": vendor,
+        "speedup_vs_torch_sparse_gpu": (vendor["ms"] / wall_ms) if vendor.get("ms") else None,
+        "rocsparse": roc,
+        "speedup_vs_rocsparse": (roc["ms"] / wall_ms) if roc.get("ms") else None,
     }
     if label in ra_spmm.TILE_KERNELS and not label.endswith("_TF32") and N % 8 == 0:
         # Native 16-bit B (the fp16-B configs C3 and C4): the same plan run on
@@ -265,10 +362,94 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
             f"identical to the fp32-B call: {res['native_fp16_B']['identical_to_fp32_B_call']}")
         del B16
     if do_cpu:
-        port, ts = cpu_baselines(g, N)
-        res["cpu_port"] = port
-        res["cpu_torch_sparse"] = ts
+        Bh = B.cpu()
+        del B, C, C_base, scale
+        torch.cuda.empty_cache()
+        res["cpu_torch_sparse"] = torch_sparse_cpu(g, Bh, cpu_seconds, cpu_rows)
+        if port:
+            res["cpu_port"] = cpu_port(g, N)
     return res
+
+
+# Per-config blocks of the default run: each config at its own width and at 128.
+CONFIG_BLOCK_N = {"C1": (64, 128), "C2": (128,), "C3": (256, 128), "C4": (512, 128), "C5": (256, 128)}
+
+
+def cpu_sample_rows(g, N, flops=4e9):
+    """Rows of the CPU leg's sample: the first rows whose SpMM is ~`flops`
+    (about 0.05-0.15 s per torch.sparse CPU call), or the whole matrix."""
+    import numpy as np
+    want = flops / (2.0 * N)
+    if g.nnz <= want:
+        return None
+    return max(1, int(np.searchsorted(g.rowptr, want)))
+
+
+def block_of(res):
+    """The per-config summary the default JSON line carries."""
+    frac = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS
+    ts = res.get("torch_sparse_gpu") or {}
+    cpu = res.get("cpu_torch_sparse") or {}
+    b = {
+        "path": res["path"], "ms": round(res["ms_per_step"], 5), "gflops": round(res["gflops"], 2),
+        "roofline": {"kernel": res["kernel"], "kernel_ms": round(res["kernel_ms"], 5),
+                     "bytes_alg": res["bytes_alg"], "frac": round(frac, 4)},
+        "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
+                 "first_exec_ms": round(res["cold_first_exec_ms"], 4)},
+        "baseline_kernel_ms": round(res["baseline_ms"], 5),
+        "speedup_vs_baseline_kernel": round(res["speedup_vs_baseline"], 3),
+        "rocsparse_ms": round(res["rocsparse"]["ms"], 5) if res["rocsparse"].get("ms") else None,
+        "rocsparse_alg": res["rocsparse"].get("alg"),
+        "speedup_vs_rocsparse": round(res["speedup_vs_rocsparse"], 3) if res.get("speedup_vs_rocsparse") else None,
+        "torch_sparse_gpu_ms": round(ts["ms"], 5) if ts.get("ms") else None,
+        "speedup_vs_torch_sparse_gpu": round(res["speedup_vs_torch_sparse_gpu"], 3)
+        if res.get("speedup_vs_torch_sparse_gpu") else None,
+        "max_rel_err_vs_baseline_kernel": res["max_rel_err_vs_baseline"],
+        "cpu_torch_sparse_gflops": round(cpu["value"], 2) if cpu else None,
+        "cpu_sample": cpu.get("sample"),
+    }
+    if ts.get("error"):
+        b["torch_sparse_gpu_error"] = ts["error"]
+    if "native_fp16_B" in res:
+        n16 = res["native_fp16_B"]
+        b["native_fp16_B"] = {"ms": round(n16["ms_per_step"], 5), "gflops": round(n16["gflops"], 2),
+                              "roofline_frac": round(n16["roofline_frac"], 4)}
+    return b
+
+
+def config_blocks(cfgs, table, steps, warmup, headline=None):
+    """Every config of BASELINE at its own N and at N=128: routed path, warm
+    time, roofline of the dominant kernel, cold costs, the baseline kernel and
+    torch.sparse on the GPU as comparators, torch.sparse CPU on a row sample."""
+    import math
+    import torch
+    from ra_spmm import synthetic as S
+    S.use_device_sort("cuda")
+    blocks = {}
+    for cfg in cfgs:
+        t0 = time.perf_counter()
+        g = S.CONFIGS[cfg]()
+        log(f"[bench] {cfg}: {g.name} M={g.M} nnz={g.nnz} generated in {time.perf_counter() - t0:.1f} s")
+        for N in CONFIG_BLOCK_N[cfg]:
+            if headline is not None and headline["config"] == cfg and headline["N"] == N:
+                res = headline
+            else:
+                res = bench_config(cfg, N, steps, warmup, table, True, cold_reps=3, g=g,
+                                   cpu_seconds=1.0, cpu_rows=cpu_sample_rows(g, N), port=False)
+            blocks[f"{cfg}_N{N}"] = block_of(res)
+            log(f"[bench] {cfg} N={N}: {json.dumps(blocks[f'{cfg}_N{N}'])}")
+            torch.cuda.empty_cache()
+        del g
+        torch.cuda.empty_cache()
+
+    def geomean(key):
+        v = [b[key] for b in blocks.values() if b.get(key)]
+        return round(math.exp(sum(math.log(x) for x in v) / len(v)), 3) if v else None
+    summary = {"geomean_speedup_vs_rocsparse": geomean("speedup_vs_rocsparse"),
+               "geomean_speedup_vs_baseline_kernel": geomean("speedup_vs_baseline_kernel"),
+               "geomean_speedup_vs_torch_sparse_gpu": geomean("speedup_vs_torch_sparse_gpu"),
+               "points": len(blocks)}
+    return blocks, summary
 
 
 def profile_traffic(kernel: str, cfg: str, N: int):
@@ -411,7 +592,14 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--config", default=None, choices=["C1", "C2", "C3", "C4", "C5"],
+                    help="measure this config alone (default: C2 as the headline, plus every config's block)")
+    ap.add_argument("--configs", default=None,
+                    help="comma-separated configs for the per-config blocks "
+                         "(default: C1,C2,C3,C4,C5 when --config is not given)")
+    ap.add_argument("--no-configs", action="store_true", help="headline line only, no per-config blocks")
+    ap.add_argument("--gather-probe", action="store_true",
+                    help="run a random-row gather of known size first (PMC scale for gathers)")
     ap.add_argument("--N", type=int, default=128)
     ap.add_argument("--table", default="mi355x", choices=["mi355x", "reference"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -452,30 +640,41 @@ def main(argv=None):
 
     if args.copy_probe:
         copy_probe()
-    res = bench_config(args.config, args.N, args.steps, args.warmup, args.table, not args.no_cpu,
+    if args.gather_probe:
+        gather_probe()
+    cfg = args.config or "C2"
+    res = bench_config(cfg, args.N, args.steps, args.warmup, args.table, not args.no_cpu,
                        force_path=args.path)
+    blocks = summary = None
+    cfgs = args.configs.split(",") if args.configs else ([] if args.config else list(CONFIG_BLOCK_N))
+    if cfgs and not args.no_configs and not args.path:
+        blocks, summary = config_blocks(cfgs, args.table, max(10, min(args.steps, 50)),
+                                        max(2, min(args.warmup, 5)), headline=res)
     achieved = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9
     copy_gbs = hbm_copy_gbs()
-    traffic = args.traffic if args.traffic is not None else profile_traffic(res["kernel"], args.config, res["N"])
+    traffic = args.traffic if args.traffic is not None else profile_traffic(res["kernel"], cfg, res["N"])
+    l2_miss_gbs = traffic / (res["kernel_ms"] * 1e-3) / 1e9 if traffic else None
     line = {
         "metric": METRIC, "value": round(res["gflops"], 3), "unit": "GFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded generator, ra_spmm.synthetic)",
-        "config": {"workload": f"{args.config} {res['graph']} M={res['M']} nnz={res['nnz']} "
+        "config": {"workload": f"{cfg} {res['graph']} M={res['M']} nnz={res['nnz']} "
                                f"N={res['N']} fp32, routed ({res['path']})",
                    "N": res["N"], "router_table": args.table},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": res["kernel"],
                      "kernel_ms": round(res["kernel_ms"], 5), "bytes_alg": res["bytes_alg"],
-                     # HBM bytes the kernel actually moves (rocprofv3 FETCH + WRITE per
-                     # launch) over this run's launch time, against the same peak.
-                     "traffic_gbs": round(traffic / (res["kernel_ms"] * 1e-3) / 1e9, 1) if traffic else None,
-                     "traffic_frac": round(traffic / (res["kernel_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+                     # rocprofv3 FETCH_SIZE + WRITE_SIZE per launch counts the L2's
+                     # requests to the fabric, which the 256 MB Infinity Cache (MALL)
+                     # serves in part: it is L2-miss traffic, not HBM bytes.  Its rate
+                     # is set beside the HBM peak only for scale.
+                     "l2_miss_traffic_gbs": round(l2_miss_gbs, 1) if traffic else None,
+                     "l2_miss_traffic_over_hbm_peak": round(l2_miss_gbs / HBM_PEAK_GBS, 4)
                      if traffic else None,
                      "measured_copy_gbs": round(copy_gbs, 1)},
-        "cpu_baseline": res.get("cpu_port"),
+        "cpu_baseline": res.get("cpu_torch_sparse"),
         "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
                  "first_exec_ms": round(res["cold_first_exec_ms"], 4),
                  # SpMM calls after which routing + plan build is repaid against
@@ -487,10 +686,18 @@ def main(argv=None):
         "baseline_csr_gflops": round(res["baseline_gflops"], 3),
         "csr_direct_gflops": round(res["csr_direct_gflops"], 3),
         "speedup_vs_baseline_kernel": round(res["speedup_vs_baseline"], 4),
+        "rocsparse": res.get("rocsparse"),
+        "speedup_vs_rocsparse": round(res["speedup_vs_rocsparse"], 4) if res.get("speedup_vs_rocsparse") else None,
+        "torch_sparse_gpu": res.get("torch_sparse_gpu"),
+        "speedup_vs_torch_sparse_gpu": round(res["speedup_vs_torch_sparse_gpu"], 4)
+        if res.get("speedup_vs_torch_sparse_gpu") else None,
         "edgewise_gbs": round(res["bytes_edgewise"] / (res["ms_per_step"] * 1e-3) / 1e9, 1),
         "max_rel_err_vs_baseline": res["max_rel_err_vs_baseline"],
-        "cpu_torch_sparse": res.get("cpu_torch_sparse"),
+        "cpu_port": res.get("cpu_port"),
     }
+    if blocks is not None:
+        line["configs"] = blocks
+        line["configs_summary"] = summary
     if "native_fp16_B" in res:
         line["native_fp16_B"] = res["native_fp16_B"]
     if args.details:

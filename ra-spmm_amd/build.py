@@ -74,6 +74,16 @@ def build_library(jobs: int) -> Path:
     return lib
 
 
+def build_vendor() -> Path:
+    """The rocSPARSE comparator (csrc/vendor_spmm.cpp): a measurement tool
+    for bench.py, kept out of the product library."""
+    out = OUT_DIR / "libra_vendor_spmm.so"
+    _run([HIPCC, "-O2", "-fPIC", "-shared", "-std=c++17", "-x", "c++", "-D__HIP_PLATFORM_AMD__=1",
+          "-I/opt/rocm/include", str(CSRC / "vendor_spmm.cpp"), "-o", str(out),
+          "-L/opt/rocm/lib", "-lrocsparse", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"])
+    return out
+
+
 def build_binding() -> Path:
     import torch  # noqa: F401  (headers and libraries of the running torch)
     from torch.utils import cpp_extension
@@ -104,6 +114,7 @@ def main(argv=None) -> None:
     args = ap.parse_args(argv)
     lib = build_library(args.jobs)
     print(f"built {lib}")
+    print(f"built {build_vendor()}")
     if not args.no_binding:
         print(f"built {build_binding()}")
 
