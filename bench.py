@@ -176,6 +176,32 @@ def rocsparse_gpu(rp, ci, vl, B, C_ref, steps):
     return out
 
 
+def gather_ceiling(ci, B, steps):
+    """The gather probe (ra_spmm.measure) over this matrix's column indices in
+    CSR order, and over as many uniform random indices: ms per pass and the
+    rate of requested B bytes.  A row-gathering SpMM on the matrix moves at
+    least these rows; the probe does nothing else."""
+    import torch
+    from ra_spmm import measure
+    N = int(B.shape[1])
+    if N % 4 or N > 256 or (N // 4) & (N // 4 - 1):
+        return None
+    out = {}
+    gen = torch.Generator(device=B.device).manual_seed(99)
+    uni = torch.randint(0, B.shape[0], (ci.numel(),), device=B.device, dtype=torch.int32, generator=gen)
+    for name, idx in (("csr_order", ci), ("uniform", uni)):
+        best = None
+        for span in (32, 256):  # the faster walk is the ceiling
+            p = measure.GatherProbe(B, idx, span)
+            _, ev = timed_steps(p.run, steps, 3)
+            if best is None or ev < best["ms"]:
+                best = {"ms": ev, "requested_gbs": p.bytes / (ev * 1e-3) / 1e9, "span": span}
+            del p
+        out[name] = best
+    del uni
+    return out
+
+
 def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
     """Mean launch time of the dominant kernel of `label`, HIP events on the
     current stream (the stream every ra_spmm launch uses)."""
@@ -313,6 +339,7 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
     flops = 2.0 * g.nnz * N
     gflops = flops / (wall_ms * 1e-3) / 1e9
     k_ms, k_name = kernel_time_ms(label, plan, rp, ci, vl, B, steps)
+    ceiling = gather_ceiling(ci, B, max(5, steps // 4)) if k_name in ("zo_fused_kernel", "csr_rows_kernel") else None
     # the MFMA kernels read 16-bit B and stored values
     b_alg = bytes_alg(g.M, g.K, g.nnz, N, *((2, 2) if k_name.startswith("tile_mfma") else (4, 4)))
 
@@ -342,6 +369,7 @@ def bench_config(cfg, N, steps, warmup, table, do_cpu, cold_reps=10, force_path=
         "max_rel_err_vs_baseline": max_rel,
         "torch_sparse_gpu": vendor,
         "speedup_vs_torch_sparse_gpu": (vendor["ms"] / wall_ms) if vendor.get("ms") else None,
+        "gather_ceiling": ceiling,
         "rocsparse": roc,
         "speedup_vs_rocsparse": (roc["ms"] / wall_ms) if roc.get("ms") else None,
     }
@@ -410,6 +438,10 @@ def block_of(res):
     }
     if ts.get("error"):
         b["torch_sparse_gpu_error"] = ts["error"]
+    if res.get("gather_ceiling"):
+        gc = res["gather_ceiling"]["csr_order"]
+        b["roofline"]["gather_probe_ms"] = round(gc["ms"], 5)
+        b["roofline"]["frac_of_gather_probe"] = round(gc["ms"] / res["kernel_ms"], 4)
     if "native_fp16_B" in res:
         n16 = res["native_fp16_B"]
         b["native_fp16_B"] = {"ms": round(n16["ms_per_step"], 5), "gflops": round(n16["gflops"], 2),
@@ -673,7 +705,12 @@ def main(argv=None):
                      "l2_miss_traffic_gbs": round(l2_miss_gbs, 1) if traffic else None,
                      "l2_miss_traffic_over_hbm_peak": round(l2_miss_gbs / HBM_PEAK_GBS, 4)
                      if traffic else None,
-                     "measured_copy_gbs": round(copy_gbs, 1)},
+                     "measured_copy_gbs": round(copy_gbs, 1),
+                     # the same B rows gathered in the same order by a kernel that
+                     # does nothing else: the data-movement ceiling on this matrix
+                     "gather_probe": res.get("gather_ceiling"),
+                     "frac_of_gather_probe": round(res["gather_ceiling"]["csr_order"]["ms"] / res["kernel_ms"], 4)
+                     if res.get("gather_ceiling") else None},
         "cpu_baseline": res.get("cpu_torch_sparse"),
         "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
                  "first_exec_ms": round(res["cold_first_exec_ms"], 4),

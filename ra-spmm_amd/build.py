@@ -84,6 +84,14 @@ def build_vendor() -> Path:
     return out
 
 
+def build_probe() -> Path:
+    """The gather probe (csrc/gather_probe.hip): a measurement tool for
+    bench.py, kept out of the product library."""
+    out = OUT_DIR / "libra_gather_probe.so"
+    _run([HIPCC] + HIP_FLAGS + ["-shared", "-x", "hip", str(CSRC / "gather_probe.hip"), "-o", str(out)])
+    return out
+
+
 def build_binding() -> Path:
     import torch  # noqa: F401  (headers and libraries of the running torch)
     from torch.utils import cpp_extension
@@ -115,6 +123,7 @@ def main(argv=None) -> None:
     lib = build_library(args.jobs)
     print(f"built {lib}")
     print(f"built {build_vendor()}")
+    print(f"built {build_probe()}")
     if not args.no_binding:
         print(f"built {build_binding()}")
 

@@ -129,22 +129,37 @@ __device__ __forceinline__ int64_t logical_block(bool remap) {
     return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
 
+// Row block and column slice of this workgroup.  nslices > 0: a 1-D grid in
+// which consecutive workgroups take consecutive column slices of the same
+// rows; workgroups are dealt round-robin to the 8 XCDs, so with 8 % nslices
+// == 0 every XCD gathers one column slice of B and its L2 holds that slice
+// only.  nslices == 0: the slice is blockIdx.y (slices outermost).
+__device__ __forceinline__ int64_t block_and_slice(bool remap, int nslices, int& slice) {
+    if (nslices > 0) {
+        slice = static_cast<int>(blockIdx.x % nslices);
+        return blockIdx.x / nslices;
+    }
+    slice = blockIdx.y;
+    return logical_block(remap);
+}
+
 // ---------------------------------------------------------------- CSR_DIRECT
 template <int G, int V, int U, typename P>
 __global__ __launch_bounds__(kBlock) void csr_rows_kernel(
     const int32_t* __restrict__ rowptr, const int32_t* __restrict__ colind,
     const float* __restrict__ vals, const P* __restrict__ Bp, P* __restrict__ Cp,
     const int32_t* __restrict__ row_list, int64_t num_rows, int64_t ldp, int np, int remap,
-    int nt, int resume) {
+    int nt, int resume, int nslices) {
     constexpr int RPW = kWave / G;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int sub = lane / G;
     const int sl = lane % G;
-    const int64_t idx = (logical_block(remap) * kWavesPerBlock + wave) * RPW + sub;
+    int slice;
+    const int64_t idx = (block_and_slice(remap, nslices, slice) * kWavesPerBlock + wave) * RPW + sub;
     if (idx >= num_rows) return;  // whole lane groups leave together
     const int row = row_list ? row_list[idx] : static_cast<int>(idx);
-    const int q0 = blockIdx.y * (G * V);
+    const int q0 = slice * (G * V);
     int q[V];
 #pragma unroll
     for (int s = 0; s < V; ++s) {
@@ -210,15 +225,16 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
     const int32_t* __restrict__ chunk_rows, const int32_t* __restrict__ chunk_starts,
     const int32_t* __restrict__ chunk_slot, int num_chunks, P* __restrict__ partials,
     const int32_t* __restrict__ short_rows, int64_t num_short, int64_t ldp, int np, int remap,
-    int nt, int sole_split) {
+    int nt, int sole_split, int nslices) {
     constexpr int RPW = kWave / G;
     __shared__ P red[kWavesPerBlock][(RPW > 1 ? RPW - 1 : 1) * G * V];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int sub = lane / G;
     const int sl = lane % G;
-    const int64_t gw = logical_block(remap) * kWavesPerBlock + wave;
-    const int q0 = blockIdx.y * (G * V);
+    int slice;
+    const int64_t gw = block_and_slice(remap, nslices, slice) * kWavesPerBlock + wave;
+    const int q0 = slice * (G * V);
     int q[V];
 #pragma unroll
     for (int s = 0; s < V; ++s) {
@@ -425,8 +441,11 @@ struct LaneShape {
 // slowest dimension), so each pass gathers only a c-column slice of B;
 // RA_ZO_SOLE_SPLIT=1 splits sole ZO chunks over the wave's lane groups.
 struct CsrTuning {
-    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0, sole_split = 0;
+    int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0, sole_split = 0, xslice = 0,
+        zo_slice = -1;
     CsrTuning() {
+        if (const char* e = std::getenv("RA_ZO_SLICE")) zo_slice = std::atoi(e);
+        if (const char* e = std::getenv("RA_CSR_XSLICE")) xslice = std::atoi(e) != 0;
         if (const char* e = std::getenv("RA_ZO_SOLE_SPLIT")) sole_split = std::atoi(e) != 0;
         if (const char* e = std::getenv("RA_CSR_COLTILE")) coltile = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_LANES")) lanes = std::atoi(e);
@@ -442,9 +461,10 @@ const CsrTuning& tuning() {
 }
 
 // Lane-group shape from the number of packets per row (per column pass).
-LaneShape pick_shape(int np, int packet_elems) {
+LaneShape pick_shape(int np, int packet_elems, int slice_elems = 0) {
     const CsrTuning& t = tuning();
-    if (t.coltile > 0) np = std::min(np, std::max(1, t.coltile / packet_elems));
+    if (slice_elems > 0) np = std::min(np, std::max(1, slice_elems / packet_elems));
+    else if (t.coltile > 0) np = std::min(np, std::max(1, t.coltile / packet_elems));
     int G;
     if (t.lanes >= 4 && t.lanes <= 64 && (t.lanes & (t.lanes - 1)) == 0) G = t.lanes;
     else G = np <= 4 ? 4 : np <= 8 ? 8 : np <= 16 ? 16 : np <= 32 ? 32 : 64;
@@ -459,11 +479,16 @@ ra_status launch_csr_rows(const LaneShape& sh, dim3 grid, hipStream_t st, const 
                           const int32_t* colind, const float* vals, const P* B, P* C,
                           const int32_t* row_list, int64_t num_rows, int64_t ldp, int np, int resume) {
     const int remap = tuning().remap, nt = tuning().nt;
+    int nslices = 0;
+    if (tuning().xslice && grid.y > 1) {
+        nslices = static_cast<int>(grid.y);
+        grid = dim3(grid.x * grid.y, 1);
+    }
 #define RA_ROWS_CASE(g, v, u)                                                               \
     if (sh.G == g && sh.V == v && sh.U == u) {                                              \
         csr_rows_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(rowptr, colind, vals, B, C,    \
                                                              row_list, num_rows, ldp, np,   \
-                                                             remap, nt, resume);            \
+                                                             remap, nt, resume, nslices);   \
         RA_LAUNCH_CHECK("csr_rows_kernel");                                                 \
         return RA_OK;                                                                       \
     }
@@ -487,13 +512,19 @@ ra_status launch_zo(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_
                     const int32_t* colind, const float* vals, const P* B, P* C,
                     const int32_t* chunk_rows, const int32_t* chunk_starts,
                     const int32_t* chunk_slot, int num_chunks, P* partials,
-                    const int32_t* short_rows, int64_t num_short, int64_t ldp, int np) {
+                    const int32_t* short_rows, int64_t num_short, int64_t ldp, int np,
+                    bool xcd_slices) {
     const int remap = tuning().zo_remap, nt = tuning().nt, sole_split = tuning().sole_split;
+    int nslices = 0;
+    if (xcd_slices && grid.y > 1) {
+        nslices = static_cast<int>(grid.y);
+        grid = dim3(grid.x * grid.y, 1);
+    }
 #define RA_ZO_CASE(g, v, u)                                                                  \
     if (sh.G == g && sh.V == v && sh.U == u) {                                               \
         zo_fused_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(                                \
             rowptr, colind, vals, B, C, chunk_rows, chunk_starts, chunk_slot, num_chunks,    \
-            partials, short_rows, num_short, ldp, np, remap, nt, sole_split);                \
+            partials, short_rows, num_short, ldp, np, remap, nt, sole_split, nslices);       \
         RA_LAUNCH_CHECK("zo_fused_kernel");                                                  \
         return RA_OK;                                                                        \
     }
@@ -592,7 +623,10 @@ static ra_status zo_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t
     if (M == 0 || N == 0) return RA_OK;
     const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
     const int np = vec ? N / 4 : N;
-    const LaneShape sh = pick_shape(np, vec ? 4 : 1);
+    // Wide rows are cut into 128-column slices dealt to the XCDs (each XCD's
+    // L2 then holds half or less of every gathered B row).
+    const int zslice = tuning().zo_slice >= 0 ? tuning().zo_slice : (vec && N >= 256 ? 128 : 0);
+    const LaneShape sh = pick_shape(np, vec ? 4 : 1, zslice);
     if (plan->info.num_split_chunks > 0 && !partials) {
         RA_TRY(plan->partials.ensure((size_t)plan->info.num_split_chunks * N * sizeof(float)));
         partials = plan->partials.get<float>();
@@ -609,13 +643,13 @@ static ra_status zo_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t
                                   plan->chunk_rows, plan->chunk_starts,
                                   plan->chunk_slot, plan->info.num_chunks,
                                   reinterpret_cast<float4*>(partials), plan->short_rows,
-                                  plan->num_short_total, np, np);
+                                  plan->num_short_total, np, np, zslice > 0);
         else
             s = launch_zo<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
                                  plan->chunk_rows, plan->chunk_starts,
                                  plan->chunk_slot, plan->info.num_chunks,
                                  partials, plan->short_rows,
-                                 plan->num_short_total, np, np);
+                                 plan->num_short_total, np, np, zslice > 0);
         RA_TRY(s);
     }
     if (plan->info.num_split_rows > 0 && stage != 1) {

@@ -1,6 +1,7 @@
 """The measurement helpers bench.py relies on: the rocSPARSE comparator
-(ra_spmm.vendor, every CSR algorithm) against the oracle, and the device sort
-of the synthetic generators against the host sort."""
+(ra_spmm.vendor, every CSR algorithm) against the oracle, the gather probe
+(ra_spmm.measure) against torch, and the device sort of the synthetic
+generators against the host sort."""
 import numpy as np
 import pytest
 import torch
@@ -43,3 +44,22 @@ def test_device_sort_generates_the_same_graphs():
             np.testing.assert_array_equal(a.vals, b.vals)
     finally:
         S.use_device_sort(None)
+
+
+@pytest.mark.parametrize("N,span", [(128, 32), (256, 256), (16, 32)])
+def test_gather_probe_reads_every_indexed_row(N, span):
+    """The gather probe's lanes add up exactly the B rows the index stream
+    names: the column sums of its output equal those of B[idx]."""
+    from ra_spmm import measure
+    gen = torch.Generator(device="cuda").manual_seed(N)
+    B = torch.randn(5000, N, device="cuda", generator=gen)
+    idx = torch.randint(0, 5000, (77_777,), device="cuda", dtype=torch.int32, generator=gen)
+    p = measure.GatherProbe(B, idx, span)
+    out = p.run().view(-1, 4)
+    torch.cuda.synchronize()
+    packets = N // 4
+    lanes = out.shape[0]
+    # lane l of a wave covers packet l % packets of its group's rows
+    per_packet = out.view(lanes // packets, packets, 4).sum(0).reshape(-1)
+    want = B[idx.long()].double().sum(0)
+    torch.testing.assert_close(per_packet.double(), want, rtol=1e-4, atol=1e-2)
