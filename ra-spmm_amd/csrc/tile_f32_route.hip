@@ -20,7 +20,7 @@
 // keeps them: one CSR per column range, launched in order, each continuing
 // the chains the previous one left in C (the B rows in use stay K / P).  Rows of skewed length
 // (degree CV >= 1.5, the router's own ZERO_OVERHEAD_CSR threshold) run on a
-// ZERO_OVERHEAD_CSR plan instead, which keeps rows of <= 64 nonzeros
+// ZERO_OVERHEAD_CSR plan instead, which keeps rows of <= 256 nonzeros
 // bit-exact and sums longer rows in 256-nonzero chunks.
 #include <hipcub/hipcub.hpp>
 
