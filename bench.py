@@ -202,6 +202,39 @@ def gather_ceiling(ci, B, steps):
     return out
 
 
+def gather_sweep(out_path=None):
+    """Bare-gather rate against the size of the gathered working set: uniform
+    random rows of an fp32 [rows, N] matrix, 2^25 gathers per pass, one
+    64-lane 16-byte-per-lane load per 1 KB at N=256.  L2-resident, Infinity
+    Cache-resident and HBM-sized working sets give the gather ceilings the
+    kernels' instruction rates are compared with (~2.4 GHz assumed for cycles)."""
+    import torch
+    from ra_spmm import measure
+    rows_out = []
+    for rows, N in [(2048, 256), (16384, 256), (65536, 256), (1 << 20, 256), (2048, 128), (2048, 64), (2048, 32)]:
+        B = torch.randn(rows, N, device="cuda")
+        n = 1 << 25
+        gen = torch.Generator(device="cuda").manual_seed(rows + N)
+        idx = torch.randint(0, rows, (n,), device="cuda", dtype=torch.int32, generator=gen)
+        best = None
+        for span in (32, 256):
+            p = measure.GatherProbe(B, idx, span)
+            _, ev = timed_steps(p.run, 10, 3)
+            best = ev if best is None else min(best, ev)
+            del p
+        instr = n * N * 4 / 1024.0  # 64 lanes x 16 B
+        rec = {"rows": rows, "N": N, "working_set_MB": rows * N * 4 / 1e6, "ms": best,
+               "requested_TBps": n * N * 4 / (best * 1e-3) / 1e12,
+               "cu_cycles_per_1KB_instr": 256 * best * 1e-3 * 2.4e9 / instr}
+        rows_out.append(rec)
+        log(f"[gather-sweep] {json.dumps(rec)}")
+        del B, idx
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps(rows_out, indent=1))
+    return rows_out
+
+
 def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
     """Mean launch time of the dominant kernel of `label`, HIP events on the
     current stream (the stream every ra_spmm launch uses)."""
@@ -630,6 +663,8 @@ def main(argv=None):
                     help="comma-separated configs for the per-config blocks "
                          "(default: C1,C2,C3,C4,C5 when --config is not given)")
     ap.add_argument("--no-configs", action="store_true", help="headline line only, no per-config blocks")
+    ap.add_argument("--gather-sweep", action="store_true",
+                    help="bare-gather rate against working-set size (details on stderr / --details)")
     ap.add_argument("--gather-probe", action="store_true",
                     help="run a random-row gather of known size first (PMC scale for gathers)")
     ap.add_argument("--N", type=int, default=128)
@@ -664,6 +699,9 @@ def main(argv=None):
         if args.details:
             Path(args.details).parent.mkdir(parents=True, exist_ok=True)
             Path(args.details).write_text(json.dumps(res, indent=1))
+        return 0
+    if args.gather_sweep:
+        gather_sweep(args.details)
         return 0
     if args.sweep:
         sweep(args.sweep.split(","), [int(n) for n in args.sweep_N.split(",")], max(10, args.steps // 4),
