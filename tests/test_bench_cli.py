@@ -30,3 +30,28 @@ def test_more_than_one_gpu_is_refused():
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
     assert r.stdout.strip() == "" or not r.stdout.strip().startswith("{")
+
+
+def test_cpu_sample_rows_bounds_the_sample():
+    import numpy as np
+    from ra_spmm import synthetic as S
+    g = S.random_csr(5000, 4000, 20.0, seed=1)
+    assert bench.cpu_sample_rows(g, 128, flops=1e12) is None  # whole matrix
+    rows = bench.cpu_sample_rows(g, 128, flops=2.0 * 128 * 10_000)
+    assert rows is not None and 0 < rows < g.M
+    assert g.rowptr[rows] >= 10_000 and g.rowptr[rows - 1] < 10_000
+
+
+def test_block_of_carries_the_driver_fields():
+    res = {"path": "ZERO_OVERHEAD_CSR", "ms_per_step": 1.0, "gflops": 4000.0, "kernel": "zo_fused_kernel",
+           "kernel_ms": 0.9, "bytes_alg": 1_000_000_000, "cold_route_ms": 0.03, "cold_build_ms": 0.7,
+           "cold_first_exec_ms": 1.1, "baseline_ms": 27.0, "speedup_vs_baseline": 27.0,
+           "max_rel_err_vs_baseline": 3e-7, "rocsparse": {"ms": 1.5, "alg": "csr_nnz_split"},
+           "speedup_vs_rocsparse": 1.5, "torch_sparse_gpu": {"ms": 30.0}, "speedup_vs_torch_sparse_gpu": 30.0,
+           "cpu_torch_sparse": {"value": 33.0, "sample": "full matrix"},
+           "gather_ceiling": {"csr_order": {"ms": 0.81}, "uniform": {"ms": 1.1}}}
+    b = bench.block_of(res)
+    assert b["roofline"]["frac"] == round(1e9 / 0.9e-3 / 1e9 / 8000.0, 4)
+    assert b["roofline"]["frac_of_gather_probe"] == round(0.81 / 0.9, 4)
+    assert b["speedup_vs_rocsparse"] == 1.5 and b["rocsparse_alg"] == "csr_nnz_split"
+    assert set(b["cold"]) == {"route_ms", "build_ms", "first_exec_ms"}
