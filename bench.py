@@ -530,7 +530,8 @@ def profile_traffic(kernel: str, cfg: str, N: int):
     return None
 
 
-def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "cusparse", "zero_overhead", "csr_direct")):
+def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocsparse", "cusparse", "zero_overhead",
+                                              "csr_direct")):
     """config C5: 2-layer GCN training step (128 -> 256 -> 47) on the
     synthetic power-law operator, forward A X and backward A^T G routed per
     (transpose, N).  Reports step time per backend and the routed paths."""
@@ -679,7 +680,7 @@ def main(argv=None):
     ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
     ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
     ap.add_argument("--gcn", action="store_true", help="config 5 GCN training step (details on stderr)")
-    ap.add_argument("--gcn-backends", default="router,router_cold,cusparse,zero_overhead,csr_direct",
+    ap.add_argument("--gcn-backends", default="router,router_cold,rocsparse,cusparse,zero_overhead,csr_direct",
                     help="comma-separated GraphBackend backends timed by --gcn")
     args = ap.parse_args(argv)
 

@@ -40,6 +40,7 @@ SOURCES = {
     "tile_kernels.hip": [],
     "tile_build_gpu.hip": [],
     "zo_build_gpu.hip": [],
+    "zo_noalloc.hip": [],
     "tile_f32_route.hip": [],
 }
 LIB_NAME = "libra_spmm_hip.so"

@@ -582,35 +582,6 @@ ra_status csr_direct_launch(const int32_t* d_rowptr, const int32_t* d_colind, co
 
 }  // namespace ra
 
-// ------------------------------------------------ fixed scratch (no alloc)
-// ra_zo_plan_run_noalloc keeps the split rows' partial slots in this array
-// instead of a plan-owned allocation.  Every GPU the library runs on holds its
-// own copy for the life of the process; calls on one GPU share it (each call
-// writes every slot it reads, so nothing needs clearing), so calls that
-// overlap on one GPU race.  Host code never passes the array's name to a
-// kernel: it takes the device address from hipGetSymbolAddress, once per
-// device, and uses that.
-constexpr uint64_t kNoAllocScratchBytes = 64ull << 20;
-static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
-static std::mutex g_scratch_mutex;
-static void* g_scratch_ptr[64] = {};
-
-static ra_status noalloc_scratch(void** out) {
-    int dev = 0;
-    RA_HIP_TRY(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return ra::fail(RA_ERR_UNSUPPORTED, "noalloc scratch: device id >= 64");
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (!g_scratch_ptr[dev]) {
-        void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !p)
-            return ra::fail(RA_ERR_HIP, "noalloc scratch: hipGetSymbolAddress failed");
-        g_scratch_ptr[dev] = p;
-    }
-    *out = g_scratch_ptr[dev];
-    return RA_OK;
-}
-
 // partials: the split chunks' slot buffer ([num_split_chunks][N] fp32), or
 // NULL to use (and grow) the plan's own.
 static ra_status zo_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
@@ -668,6 +639,14 @@ static ra_status zo_run(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t
     }
     return RA_OK;
 }
+
+namespace ra {
+ra_status zo_run_with_partials(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
+                               const float* d_vals, const float* d_B, float* d_C, int32_t N, float* partials,
+                               hipStream_t st) {
+    return zo_run(plan, d_rowptr, d_colind, d_vals, d_B, d_C, N, 0, partials, st);
+}
+}  // namespace ra
 
 extern "C" {
 
@@ -858,22 +837,6 @@ ra_status ra_zo_plan_run_stage(ra_zo_plan* plan, const int32_t* d_rowptr,
                                const int32_t* d_colind, const float* d_vals, const float* d_B,
                                float* d_C, int32_t N, int32_t stage, ra_stream_t stream) {
     return zo_run(plan, d_rowptr, d_colind, d_vals, d_B, d_C, N, stage, nullptr,
-                  reinterpret_cast<hipStream_t>(stream));
-}
-
-ra_status ra_zo_plan_run_noalloc(ra_zo_plan* plan, const int32_t* d_rowptr,
-                                 const int32_t* d_colind, const float* d_vals, const float* d_B,
-                                 float* d_C, int32_t N, ra_stream_t stream) {
-    if (!plan) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo noalloc: plan is NULL");
-    if (N < 0) return ra::fail(RA_ERR_INVALID_ARGUMENT, "zo noalloc: N < 0");
-    const uint64_t need = (uint64_t)plan->info.num_split_chunks * (uint64_t)N * sizeof(float);
-    if (need > kNoAllocScratchBytes)
-        return ra::fail(RA_ERR_UNSUPPORTED,
-                        "zo noalloc: the split rows need more partial-slot memory than the "
-                        "fixed 64 MiB scratch (num_split_chunks * N * 4 bytes)");
-    float* slots = nullptr;
-    if (need > 0) RA_TRY(noalloc_scratch(reinterpret_cast<void**>(&slots)));
-    return zo_run(plan, d_rowptr, d_colind, d_vals, d_B, d_C, N, 0, slots,
                   reinterpret_cast<hipStream_t>(stream));
 }
 

@@ -90,6 +90,17 @@ int ra_vendor_spmm_run(void* plan) {
     return s == rocsparse_status_success ? 0 : fail("rocsparse compute", s);
 }
 
+// Point the plan at another B and C of the same shapes (the analysis and
+// buffer stay valid: they depend on A only).
+int ra_vendor_spmm_set_dense(void* plan, const float* d_B, float* d_C) {
+    auto* p = static_cast<VendorPlan*>(plan);
+    rocsparse_status s;
+    if ((s = rocsparse_dnmat_set_values(p->B, const_cast<float*>(d_B))) != rocsparse_status_success ||
+        (s = rocsparse_dnmat_set_values(p->C, d_C)) != rocsparse_status_success)
+        return fail("rocsparse set values", s);
+    return 0;
+}
+
 void ra_vendor_spmm_destroy(void* plan) { delete static_cast<VendorPlan*>(plan); }
 
 }  // extern "C"

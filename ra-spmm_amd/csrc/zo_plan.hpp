@@ -49,3 +49,12 @@ struct ra_zo_plan {
         return RA_OK;
     }
 };
+
+namespace ra {
+// ZERO_OVERHEAD_CSR run (both launches) with the split chunks' partial slots in
+// `partials` ([num_split_chunks][N] fp32, 16-byte aligned) instead of the
+// plan's own buffer (csr_kernels.hip).
+ra_status zo_run_with_partials(ra_zo_plan* plan, const int32_t* d_rowptr, const int32_t* d_colind,
+                               const float* d_vals, const float* d_B, float* d_C, int32_t N, float* partials,
+                               hipStream_t st);
+}  // namespace ra

@@ -16,6 +16,8 @@ per (transpose, N) and one executor (path label + plan) per
   "csr_direct", "zero_overhead", "tc_direct", "tc_direct_tf32",
   "community_tc", "segment_hybrid"   fixed paths
   "torch"         torch.sparse CSR on the device (external comparison only)
+  "rocsparse"     rocSPARSE's fastest CSR SpMM algorithm per (transpose, N),
+                  the vendor-library comparison (ra_spmm.vendor)
 """
 from __future__ import annotations
 
@@ -149,6 +151,11 @@ class GraphBackend:
             ex = ("CUSPARSE", _C.make_cusparse_plan(t["rowptr"], t["colind"], t["vals"], tmpl))
         elif backend == "torch":
             ex = ("torch", None)
+        elif backend == "rocsparse":
+            from . import vendor
+            B0 = torch.zeros((M, int(ncols)), device=self.device)
+            plan, alg = vendor.fastest(t["rowptr"], t["colind"], t["vals"], B0)
+            ex = ("rocsparse", plan)
         else:
             if backend in ("router", "router_cold"):
                 label = self.routed_label(transpose, ncols)
@@ -191,6 +198,10 @@ class GraphBackend:
         label, plan = self._get_executor(backend, transpose, ncols)
         if label == "CUSPARSE":
             return _C.run_cusparse_plan(plan, B).clone()
+        if label == "rocsparse":
+            C = torch.empty((int(t["rowptr"].numel()) - 1, ncols), device=B.device)
+            plan.rebind(B.contiguous(), C)
+            return plan.run()
         if label == "torch":
             if transpose not in self._torch_sparse:
                 M = int(t["rowptr"].numel()) - 1

@@ -28,6 +28,8 @@ def _lib():
         lib.ra_vendor_spmm_create.restype = ctypes.c_int
         lib.ra_vendor_spmm_run.argtypes = [P]
         lib.ra_vendor_spmm_run.restype = ctypes.c_int
+        lib.ra_vendor_spmm_set_dense.argtypes = [P, P, P]
+        lib.ra_vendor_spmm_set_dense.restype = ctypes.c_int
         lib.ra_vendor_spmm_destroy.argtypes = [P]
         lib.ra_vendor_spmm_destroy.restype = None
         lib.ra_vendor_last_error.restype = ctypes.c_char_p
@@ -59,6 +61,17 @@ class RocsparseSpMM:
             raise RuntimeError(f"rocsparse ({alg}): {lib.ra_vendor_last_error().decode()}")
         self._h = h
 
+    def rebind(self, B, C):
+        """Run on another B and C of the same shapes, dtype and device."""
+        old = self._keep
+        if B.shape != old[3].shape or C.shape != old[4].shape or B.dtype != torch.float32 \
+                or C.dtype != torch.float32 or not (B.is_contiguous() and C.is_contiguous()):
+            raise ValueError("rebind needs contiguous fp32 B and C of the plan's shapes")
+        st = _lib().ra_vendor_spmm_set_dense(self._h, ctypes.c_void_p(B.data_ptr()), ctypes.c_void_p(C.data_ptr()))
+        if st != 0:
+            raise RuntimeError(f"rocsparse: {_lib().ra_vendor_last_error().decode()}")
+        self._keep = old[:3] + (B, C)
+
     def run(self):
         st = _lib().ra_vendor_spmm_run(self._h)
         if st != 0:
@@ -72,3 +85,32 @@ class RocsparseSpMM:
 
     def __del__(self):
         self.close()
+
+
+def fastest(rowptr, colind, vals, B, reps: int = 5):
+    """The rocSPARSE algorithm that runs this A fastest at B's width, timed on
+    B with HIP events: (plan bound to B and a fresh C, algorithm name)."""
+    best = None
+    for alg in ALGS:
+        C = torch.empty((rowptr.numel() - 1, B.shape[1]), device=B.device)
+        try:
+            v = RocsparseSpMM(rowptr, colind, vals, B, C, alg)
+        except RuntimeError:
+            continue
+        v.run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            v.run()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        if best is None or ms < best[0]:
+            if best is not None:
+                best[1].close()
+            best = (ms, v, alg)
+        else:
+            v.close()
+    if best is None:
+        raise RuntimeError("rocsparse: no CSR algorithm accepted this matrix")
+    return best[1], best[2]

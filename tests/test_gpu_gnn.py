@@ -20,7 +20,7 @@ def _operator(M=4000, seed=3):
     return gnn.build_aggregation_operator(A, "gcn")
 
 
-@pytest.mark.parametrize("backend", ["router", "router_cold", "cusparse", "csr_direct",
+@pytest.mark.parametrize("backend", ["router", "router_cold", "cusparse", "rocsparse", "csr_direct",
                                      "zero_overhead", "tc_direct", "tc_direct_tf32",
                                      "segment_hybrid"])
 def test_validate_backend(backend):
@@ -37,7 +37,7 @@ def test_gcn_step_matches_dense_reference():
     y = torch.randint(0, 7, (M,), device="cuda")
     dense = torch.from_numpy(op.toarray()).cuda()
     results = {}
-    for backend in ("cusparse", "router", "zero_overhead", "csr_direct", "segment_hybrid"):
+    for backend in ("cusparse", "rocsparse", "router", "zero_overhead", "csr_direct", "segment_hybrid"):
         torch.manual_seed(1)
         model = gnn.GCN(32, 64, 7).cuda()
         graph = gnn.GraphBackend(op, "cuda")
