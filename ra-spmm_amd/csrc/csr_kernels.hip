@@ -118,6 +118,36 @@ __device__ __forceinline__ void accumulate_range(const int32_t* __restrict__ col
     }
 }
 
+// As accumulate_range, with the (column, value) pairs of [p0, p1) already in
+// LDS (s_col / s_val indexed from the chunk start): one broadcast LDS read per
+// pair instead of a coalesced global load and a lane shuffle.
+template <int G, int V, int U, typename P>
+__device__ __forceinline__ void accumulate_lds(const int32_t* s_col, const float* s_val,
+                                               const P* __restrict__ Bp, int64_t ldp, int p0, int p1,
+                                               const int (&q)[V], P (&acc)[V]) {
+    for (int p = p0; p < p1; p += U) {
+        int c[U];
+        float a[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            c[k] = p + k < p1 ? s_col[p + k] : 0;
+            a[k] = p + k < p1 ? s_val[p + k] : 0.f;
+        }
+        P b[U][V];
+#pragma unroll
+        for (int k = 0; k < U; ++k)
+#pragma unroll
+            for (int s = 0; s < V; ++s)
+                b[k][s] = (p + k < p1 && q[s] >= 0) ? Bp[(int64_t)c[k] * ldp + q[s]] : pzero<P>();
+#pragma unroll
+        for (int k = 0; k < U; ++k)
+            if (p + k < p1) {
+#pragma unroll
+                for (int s = 0; s < V; ++s) acc[s] = pfma(a[k], b[k][s], acc[s]);
+            }
+    }
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // With remap on, XCD x runs a contiguous range of logical blocks, so rows that
 // are close in the row order (and tend to share columns) share one L2.
@@ -225,9 +255,11 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
     const int32_t* __restrict__ chunk_rows, const int32_t* __restrict__ chunk_starts,
     const int32_t* __restrict__ chunk_slot, int num_chunks, P* __restrict__ partials,
     const int32_t* __restrict__ short_rows, int64_t num_short, int64_t ldp, int np, int remap,
-    int nt, int sole_split, int nslices) {
+    int nt, int sole_split, int nslices, int lds_stage) {
     constexpr int RPW = kWave / G;
     __shared__ P red[kWavesPerBlock][(RPW > 1 ? RPW - 1 : 1) * G * V];
+    __shared__ int s_col[kWavesPerBlock][kChunk];
+    __shared__ float s_val[kWavesPerBlock][kChunk];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int sub = lane / G;
@@ -250,12 +282,24 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
         const int row = static_cast<int>(tag & ~kSoleFlag);
         const int cs = chunk_starts[gw];
         const int ce = min(cs + kChunk, rowptr[row + 1]);
+        if (lds_stage) {
+            // The chunk's (column, value) pairs go to LDS first, in one
+            // coalesced pass by the whole wave (RA_ZO_LDS_STAGE=0: loaded G at a
+            // time and shuffled, as for the short rows).
+            for (int i = lane; i < ce - cs; i += kWave) {
+                s_col[wave][i] = load_once(colind + cs + i, nt != 0);
+                s_val[wave][i] = load_once(vals + cs + i, nt != 0);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+        }
         if ((tag & kSoleFlag) && !sole_split) {
             // A sole chunk (a row of 65..256 nonzeros) is one lane group's
             // single fma chain per element, as for the short rows: the same
             // bits as CSR_DIRECT (csr/ra_zero_overhead.cu:246-262).
             if (sub != 0) return;
-            accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, cs, ce, sl, q, acc, nt != 0);
+            if (lds_stage) accumulate_lds<G, V, U, P>(s_col[wave], s_val[wave], Bp, ldp, 0, ce - cs, q, acc);
+            else accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, cs, ce, sl, q, acc, nt != 0);
 #pragma unroll
             for (int s = 0; s < V; ++s)
                 if (q[s] >= 0) store_once(Cp + (int64_t)row * ldp + q[s], acc[s], nt != 0);
@@ -264,7 +308,8 @@ __global__ __launch_bounds__(kBlock) void zo_fused_kernel(
         constexpr int L = kChunk / RPW;
         const int a = min(cs + sub * L, ce);
         const int b = min(a + L, ce);
-        accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, a, b, sl, q, acc, nt != 0);
+        if (lds_stage) accumulate_lds<G, V, U, P>(s_col[wave], s_val[wave], Bp, ldp, a - cs, b - cs, q, acc);
+        else accumulate_range<G, V, U, P>(colind, vals, Bp, ldp, a, b, sl, q, acc, nt != 0);
         if constexpr (RPW > 1) {
             if (sub > 0) {
 #pragma unroll
@@ -439,11 +484,14 @@ struct LaneShape {
 // chunks onto one XCD), RA_CSR_STREAMING=0 turns the non-temporal hints off,
 // RA_CSR_COLTILE=c processes the columns in passes of c elements (the grid's
 // slowest dimension), so each pass gathers only a c-column slice of B;
-// RA_ZO_SOLE_SPLIT=1 splits sole ZO chunks over the wave's lane groups.
+// RA_ZO_SOLE_SPLIT=1 splits sole ZO chunks over the wave's lane groups;
+// RA_ZO_LDS_STAGE=0 turns off the LDS staging of the chunks' (column, value)
+// pairs.
 struct CsrTuning {
     int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0, sole_split = 0, xslice = 0,
-        zo_slice = -1;
+        zo_slice = -1, lds_stage = 1;
     CsrTuning() {
+        if (const char* e = std::getenv("RA_ZO_LDS_STAGE")) lds_stage = std::atoi(e) != 0;
         if (const char* e = std::getenv("RA_ZO_SLICE")) zo_slice = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_XSLICE")) xslice = std::atoi(e) != 0;
         if (const char* e = std::getenv("RA_ZO_SOLE_SPLIT")) sole_split = std::atoi(e) != 0;
@@ -524,7 +572,8 @@ ra_status launch_zo(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_
     if (sh.G == g && sh.V == v && sh.U == u) {                                               \
         zo_fused_kernel<g, v, u, P><<<grid, kBlock, 0, st>>>(                                \
             rowptr, colind, vals, B, C, chunk_rows, chunk_starts, chunk_slot, num_chunks,    \
-            partials, short_rows, num_short, ldp, np, remap, nt, sole_split, nslices);       \
+            partials, short_rows, num_short, ldp, np, remap, nt, sole_split, nslices,        \
+            tuning().lds_stage);                                                             \
         RA_LAUNCH_CHECK("zo_fused_kernel");                                                  \
         return RA_OK;                                                                        \
     }
