@@ -73,7 +73,7 @@ def test_csr_direct_unaligned_B_uses_scalar_path(oracle):
     np.testing.assert_array_equal(C.cpu().numpy(), oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B))
 
 
-@pytest.mark.parametrize("N", [32, 36, 44, 47, 48, 64, 128, 256, 512])
+@pytest.mark.parametrize("N", [32, 36, 44, 47, 48, 64, 128, 256, 260, 384, 512, 1000])
 def test_zero_overhead_hub_rows(oracle, N):
     print(f"[zo] N={N}", flush=True)
     # Power-law rows: tiny/short/medium/long bins plus multi-chunk hubs.
