@@ -606,6 +606,7 @@ def sweep(configs, Ns, steps, out_path):
     from ra_spmm import synthetic as S
     rows = []
     for cfg in configs:
+        S.use_device_sort("cuda")
         g = S.CONFIGS[cfg]()
         rp, ci, vl = g.torch("cuda")
         host = (rp.cpu(), ci.cpu(), vl.cpu())  # plan builders take host CSR, as in the reference
@@ -614,6 +615,12 @@ def sweep(configs, Ns, steps, out_path):
             base = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
             scale = ra_spmm.spmm_csr_baseline(rp, ci, vl.abs(), B.abs())
             routed = ra_spmm.route_label(ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N, "MAIN", "mi355x"))
+            roc = rocsparse_gpu(rp, ci, vl, B, base, max(5, steps // 2))
+            if roc.get("ms"):
+                rows.append({"config": cfg, "N": N, "path": "ROCSPARSE", "ms": roc["ms"],
+                             "gflops": 2.0 * g.nnz * N / (roc["ms"] * 1e-3) / 1e9, "alg": roc["alg"],
+                             "routed": False})
+                log(f"[sweep] {cfg} N={N:4d} {'ROCSPARSE':22s} {roc['ms']:9.3f} ms ({roc['alg']})")
             for label in ["CSR_BASELINE"] + ra_spmm.DEPLOYED_KERNELS:
                 if label in ra_spmm.TILE_KERNELS and N < 16:
                     continue
