@@ -110,7 +110,7 @@ def build_binding() -> Path:
             "-DTORCH_API_INCLUDE_EXTENSION_H"]
            + incs + ["-I", py_inc, "-I", "/opt/rocm/include", str(CSRC / "torch_binding.cpp"),
                      "-o", str(out), "-L", str(OUT_DIR), "-lra_spmm_hip", "-L", str(torch_lib),
-                     "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+                     "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-L/opt/rocm/lib", "-lamdhip64",
                      "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"])
     _run(cmd)
     return out

