@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 import ra_spmm  # noqa: E402
 
 
-@pytest.mark.parametrize("n,dtype", [(1000, torch.int32), ((32 << 20) // 4, torch.float32),
+@pytest.mark.parametrize("n,dtype", [(1000, torch.int32), ((4 << 20) // 4 + 5, torch.int32), ((32 << 20) // 4, torch.float32),
                                      ((48 << 20) // 4 + 3, torch.int32), ((100 << 20) // 4 + 1, torch.float32)])
 def test_upload_equals_torch_copy(n, dtype):
     rng = np.random.default_rng(n)
