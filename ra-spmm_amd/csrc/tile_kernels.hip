@@ -40,6 +40,7 @@ constexpr int kBlock = kWave * kWavesPerBlock;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -383,6 +384,119 @@ __global__ __launch_bounds__(kBlock) void tile_mfma_tall_kernel(
     }
 }
 
+// ------------------------------ MFMA route, 32-row windows on 32x32x16 MFMA
+// The 32-row tall layout run with v_mfma_f32_32x32x16_{f16,bf16}: lane
+// (j = lane & 31, q = lane >> 5) feeds row j over k = 8q..8q+7 of a half block
+// (16 vectors) as the A operand and gathers B columns col0 + 8j .. +7 of those
+// 8 vectors (one 16-byte load each, register transpose) as the B operand.  A
+// wave covers 256 columns: each 64-lane gather reads 2 B rows of 512 bytes
+// instead of 4 rows of 256 bytes, and a block's A values are read once per
+// 256 columns instead of once per 128.  D of MFMA cc: lane holds rows
+// 8(i/4) + 4q + i%4 (i < 16) of column col0 + 8j + cc.
+template <bool BF16>
+__device__ __forceinline__ f32x16 mfma3232(u16x8 a, u16x8 b, f32x16 c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <bool BF16, int KIND>
+__global__ __launch_bounds__(kBlock, 2) void tile_mfma_tall32_kernel(
+    Items it, const int32_t* __restrict__ atox, const uint16_t* __restrict__ vals,
+    const uint16_t* __restrict__ Bh, int ldb, float* __restrict__ C, float* __restrict__ scratch,
+    int M, int N, int num_items, int nslices, int order, float unscale, int vec_store) {
+    constexpr int H = 32;
+    constexpr int BV = H * 32;  // values per block
+    const int lane = threadIdx.x & (kWave - 1);
+    int64_t item_blk;
+    int slice;
+    tile_block_coords(nslices, order, item_blk, slice);
+    const int item = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(item_blk * kWavesPerBlock + (threadIdx.x >> 6)));
+    if (item >= num_items) return;
+    int w, b0, b1, slot;
+    item_range(it, item, w, b0, b1, slot);
+    const int j = lane & 31;
+    const int q = lane >> 5;
+    const int col = slice * 256 + j * 8;
+    const bool col_ok = col < ldb;
+    // A operand of row j, k-group q4: offset in the [2][4][16][8] block layout.
+    const int a_row = ((j >> 4) * 4) * 16 + (j & 15);
+
+    f32x16 acc[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[cc][i] = 0.f;
+
+    // Column indices: one 16-byte load per lane covers blocks [c0, c0 + 8);
+    // block s, k-group q4 sits in lanes 8s + 2q4 and 8s + 2q4 + 1.
+    auto load_chunk = [&](int c0) {
+        int4 v = make_int4(-1, -1, -1, -1);
+        if (c0 + (lane >> 3) < b1) v = *reinterpret_cast<const int4*>(atox + (int64_t)c0 * 32 + lane * 4);
+        return v;
+    };
+    int4 chunk = load_chunk(b0), chunk_next = make_int4(-1, -1, -1, -1);
+    for (int b = b0; b < b1; ++b) {
+        const int s = (b - b0) & 7;
+        if (s == 0 && b + 8 < b1) chunk_next = load_chunk(b + 8);
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) {
+            const int q4 = 2 * h + q;
+            int cols[8];
+            const int l0 = 8 * s + 2 * q4;
+            cols[0] = __shfl(chunk.x, l0, kWave);
+            cols[1] = __shfl(chunk.y, l0, kWave);
+            cols[2] = __shfl(chunk.z, l0, kWave);
+            cols[3] = __shfl(chunk.w, l0, kWave);
+            cols[4] = __shfl(chunk.x, l0 + 1, kWave);
+            cols[5] = __shfl(chunk.y, l0 + 1, kWave);
+            cols[6] = __shfl(chunk.z, l0 + 1, kWave);
+            cols[7] = __shfl(chunk.w, l0 + 1, kWave);
+            const u16x8 a = *reinterpret_cast<const u16x8*>(vals + (int64_t)b * BV + (a_row + q4 * 16) * 8);
+            u16x8 raw[8];
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                if (cols[v] >= 0 && col_ok)
+                    raw[v] = *reinterpret_cast<const u16x8*>(Bh + (int64_t)cols[v] * ldb + col);
+                else
+                    raw[v] = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int cc = 0; cc < 8; ++cc) {
+                u16x8 bop;
+#pragma unroll
+                for (int v = 0; v < 8; ++v) bop[v] = raw[v][cc];
+                acc[cc] = mfma3232<BF16>(a, bop, acc[cc]);
+            }
+        }
+        if (s == 7) chunk = chunk_next;
+    }
+
+    const bool vec = vec_store && col + 8 <= N;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int m = 8 * (i >> 2) + 4 * q + (i & 3);
+        float* dst = item_row<KIND, H>(it, C, scratch, w, slot, m, M, N);
+        if (!dst) continue;
+        float out[8];
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) out[cc] = acc[cc][i] * unscale;  // exact: power of two
+        const bool add = it.accumulate && slot < 0;
+        if (vec) {
+            put4(dst + col, f32x4{out[0], out[1], out[2], out[3]}, add);
+            put4(dst + col + 4, f32x4{out[4], out[5], out[6], out[7]}, add);
+        } else {
+#pragma unroll
+            for (int cc = 0; cc < 8; ++cc)
+                if (col + cc < N) put1(dst + col + cc, out[cc], add);
+        }
+    }
+}
+
 // ------------------------------------------------ SEGMENT_HYBRID merge
 // C[w*8+m][n] = ((slot0 + slot1) + ...) in ascending slot order
 // (tc/ra_segment_hybrid.cu:198-221).
@@ -594,6 +708,40 @@ ra_status launch_mfma_tall(const ra_tile_plan* p, const Part& part, const uint16
     return RA_OK;
 }
 
+// 32-row windows run on the 32x32x16 MFMA kernel at N >= 512 (C3 N=512:
+// 1.048 -> 0.968 ms; at N=256 its two waves per SIMD, one per window, lose:
+// 0.498 -> 0.533 ms).  RA_TILE_MFMA32=1 forces it at N > 128, 0 turns it off.
+bool tile_use_mfma32(int N) {
+    static const int v = [] {
+        const char* e = std::getenv("RA_TILE_MFMA32");
+        return e ? std::atoi(e) : -1;
+    }();
+    if (v == 0) return false;
+    if (v == 1) return N > 128;
+    return N >= 512;
+}
+
+template <int KIND>
+ra_status launch_mfma_tall32(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, bool bf16,
+                             float* C, float* scratch, int N, hipStream_t st) {
+    const int M = p->info.M;
+    const Items it = plan_items(p, part);
+    const int nslices = (N + 255) / 256;
+    const int order = (KIND == RA_TILE_COMMUNITY_TC ? 0 : tile_remap()) |
+                      (tile_slice_major(nslices, KIND != RA_TILE_COMMUNITY_TC && tile_remap()) ? 2 : 0);
+    const float unscale = std::ldexp(1.0f, -p->info.value_scale_log2);
+    dim3 grid(static_cast<unsigned>(((int64_t)part.num_items + kWavesPerBlock - 1) / kWavesPerBlock * nslices));
+    const int vec_store = (N % 4 == 0) && ra::aligned16(C) && (!scratch || ra::aligned16(scratch));
+    if (bf16)
+        tile_mfma_tall32_kernel<true, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),
+            p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, part.num_items, nslices, order, unscale, vec_store);
+    else
+        tile_mfma_tall32_kernel<false, KIND><<<grid, kBlock, 0, st>>>(it, p->atox.get<int32_t>(),
+            p->vals.get<uint16_t>(), Bh, ldb, C, scratch, M, N, part.num_items, nslices, order, unscale, vec_store);
+    RA_LAUNCH_CHECK("tile_mfma_tall32_kernel");
+    return RA_OK;
+}
+
 template <int KIND>
 ra_status launch_kind(const ra_tile_plan* p, const Part& part, const uint16_t* Bh, int ldb, bool bf16, float* C,
                       float* scratch, int N, hipStream_t st) {
@@ -602,6 +750,7 @@ ra_status launch_kind(const ra_tile_plan* p, const Part& part, const uint16_t* B
         case 16:
             return launch_mfma_tall<KIND, 1>(p, part, Bh, ldb, bf16, C, scratch, N, st);
         case 32:
+            if (tile_use_mfma32(N)) return launch_mfma_tall32<KIND>(p, part, Bh, ldb, bf16, C, scratch, N, st);
             return launch_mfma_tall<KIND, 2>(p, part, Bh, ldb, bf16, C, scratch, N, st);
         default:
             return launch_mfma_kind<KIND>(p, part, Bh, ldb, bf16, C, scratch, N, st);

@@ -72,7 +72,7 @@ def test_tall_plan_decodes_to_matrix(oracle, rows, kind, gname):
 @pytest.mark.parametrize("gname", list(GRAPHS))
 @pytest.mark.parametrize("kind", [0, 1, 2])
 @pytest.mark.parametrize("rows", [16, 32])
-@pytest.mark.parametrize("N", [16, 47, 128, 256])
+@pytest.mark.parametrize("N", [16, 47, 128, 256, 520])
 def test_tall_routes(oracle, gname, kind, rows, N):
     print(f"[tall] {gname} kind={kind} rows={rows} N={N}", flush=True)
     g = GRAPHS[gname]()
@@ -92,10 +92,10 @@ def test_tall_routes(oracle, gname, kind, rows, N):
 
 
 @pytest.mark.parametrize("rows", [16, 32])
-def test_tall_bf16_and_lowp(oracle, rows):
+@pytest.mark.parametrize("N", [128, 512])  # 32-row windows at N >= 512 run on the 32x32x16 MFMA kernel
+def test_tall_bf16_and_lowp(oracle, rows, N):
     g = GRAPHS["community"]()
     rp, ci, vl = g.torch("cuda")
-    N = 128
     B = np.random.default_rng(9).standard_normal((g.K, N)).astype(np.float32)
     Bd = torch.from_numpy(B).cuda()
     plan = ra_spmm.make_tc_direct_plan(rp, ci, vl, g.M, g.K, N, "bf16", rows_per_window=rows)
