@@ -20,6 +20,7 @@ fp32 N(0,1) (synthetic, seeded), C = A @ B through the MI355X router.
   configs   every BASELINE config (C1..C5) at its own N and at N=128, each
             with its path, warm time, roofline, cold costs, comparators and
             torch.sparse CPU on a row sample; geomean speed-ups over them
+  gcn       config 5's GCN training step, routed and on rocSPARSE
 
 --config C1..C5 measures one config alone.  --sweep times every deployed path
 on the chosen configs (calibration of the router table).
@@ -531,7 +532,7 @@ def profile_traffic(kernel: str, cfg: str, N: int):
 
 
 def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocsparse", "cusparse", "zero_overhead",
-                                              "csr_direct")):
+                                              "csr_direct"), order_auto=True):
     """config C5: 2-layer GCN training step (128 -> 256 -> 47) on the
     synthetic power-law operator, forward A X and backward A^T G routed per
     (transpose, N).  Reports step time per backend and the routed paths."""
@@ -540,6 +541,7 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
     import torch
     from ra_spmm import gnn
     from ra_spmm import synthetic as S
+    S.use_device_sort("cuda")
     g = S.CONFIGS["C5"]()
     op = sp.csr_matrix((g.vals, g.colind, g.rowptr), shape=(g.M, g.M))
     torch.manual_seed(0)
@@ -578,7 +580,7 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
             f"{rec.get('paths', '')}")
         del graph, model, opt
         torch.cuda.empty_cache()
-    if "router" in backends:
+    if "router" in backends and order_auto:
         # The same model with order="auto": layer 1 aggregates before its
         # linear map (SpMM at N=128, no backward SpMM).  Reported beside the
         # reference-order step, never in its place.
@@ -671,6 +673,7 @@ def main(argv=None):
                     help="comma-separated configs for the per-config blocks "
                          "(default: C1,C2,C3,C4,C5 when --config is not given)")
     ap.add_argument("--no-configs", action="store_true", help="headline line only, no per-config blocks")
+    ap.add_argument("--no-gcn", action="store_true", help="leave the C5 GCN step out of the default run")
     ap.add_argument("--gather-sweep", action="store_true",
                     help="bare-gather rate against working-set size (details on stderr / --details)")
     ap.add_argument("--gather-probe", action="store_true",
@@ -728,6 +731,16 @@ def main(argv=None):
     if cfgs and not args.no_configs and not args.path:
         blocks, summary = config_blocks(cfgs, args.table, max(10, min(args.steps, 50)),
                                         max(2, min(args.warmup, 5)), headline=res)
+    gcn = None
+    if not args.config and not args.no_configs and not args.no_gcn:
+        # Config 5's GCN training step, routed and on rocSPARSE (bench --gcn has every backend).
+        g5 = bench_gcn(10, 3, args.table, ("router", "rocsparse"), order_auto=False)
+        gcn = {"model": "2-layer GCN 128 -> 256 -> 47, 4 routed SpMMs per step", "graph": g5["graph"],
+               "nnz": g5["nnz"], "router_step_ms": round(g5["router"]["step_ms"], 3),
+               "router_cold_first_step_ms": round(g5["router"]["cold_first_step_ms"], 2),
+               "router_paths": g5["router"]["paths"],
+               "rocsparse_step_ms": round(g5["rocsparse"]["step_ms"], 3),
+               "speedup_vs_rocsparse": round(g5["rocsparse"]["step_ms"] / g5["router"]["step_ms"], 3)}
     achieved = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9
     copy_gbs = hbm_copy_gbs()
     traffic = args.traffic if args.traffic is not None else profile_traffic(res["kernel"], cfg, res["N"])
@@ -781,6 +794,8 @@ def main(argv=None):
     if blocks is not None:
         line["configs"] = blocks
         line["configs_summary"] = summary
+    if gcn is not None:
+        line["gcn_step_C5"] = gcn
     if "native_fp16_B" in res:
         line["native_fp16_B"] = res["native_fp16_B"]
     if args.details:
