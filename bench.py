@@ -685,7 +685,7 @@ def main(argv=None):
                     help="HBM bytes per launch of the dominant kernel from rocprofv3 --pmc")
     ap.add_argument("--sweep", default=None, help="comma-separated configs to sweep all paths on")
     ap.add_argument("--sweep-N", default="64,128,256")
-    ap.add_argument("--sweep-out", default="gpurun_out/sweep.json")
+    ap.add_argument("--sweep-out", default=None, help="write the sweep rows here as JSON")
     ap.add_argument("--details", default=None, help="write the full result dict here")
     ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
     ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
