@@ -131,12 +131,13 @@ def test_inactive_plan_raises_and_families_agree(oracle):
     np.testing.assert_array_equal(outs[0].cpu().numpy(), outs[2].cpu().numpy())
 
 
-def test_c3_full_size_properties(oracle):
+@pytest.mark.parametrize("N", [256, 512])  # 32-row windows run on the 32x32x16 MFMA kernel at N >= 512
+def test_c3_full_size_properties(oracle, N):
     """config C3 (SBM, fp16 values) at full size through TC_DIRECT and
     COMMUNITY_TC: a row sample against the oracle, and all-ones row sums."""
+    print(f"[c3 full] N={N}", flush=True)
     g = S.CONFIGS["C3"]()
     gd = g.torch("cuda")
-    N = 256
     rng = np.random.default_rng(2)
     B = rng.standard_normal((g.K, N)).astype(np.float16).astype(np.float32)
     Bd = torch.from_numpy(B).cuda()
