@@ -255,6 +255,9 @@ def kernel_time_ms(label, plan, rp, ci, vl, B, steps):
         Bh = B.half()  # build_kernel_plan stores fp16 values
         fn = lambda: ra_spmm.run_tile_plan_route(plan, Bh, "fp16")  # noqa: E731
         name = "tile_mfma_tall_kernel" if plan.rows_per_window in (16, 32) else "tile_mfma_kernel"
+        m32 = os.environ.get("RA_TILE_MFMA32", "")
+        if plan.rows_per_window == 32 and m32 != "0" and (B.shape[1] >= 512 or (m32 == "1" and B.shape[1] > 128)):
+            name = "tile_mfma_tall32_kernel"  # the library's choice for 32-row windows at this width
     else:
         fn = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
         name = "tile path (total)"
