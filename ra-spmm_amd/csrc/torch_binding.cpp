@@ -63,8 +63,9 @@ void check_plan_device(int plan_device, const torch::Tensor& B) {
 // tensors of 1 MiB and more go through two pinned 16 MiB staging buffers: the
 // (multi-threaded) host copy of chunk i+1 overlaps the DMA of chunk i, which
 // moves 128 MB in ~2.7 ms against ~4.9 ms for a plain pageable copy.  The
-// staging buffers are allocated once per process; their events (one pair per
-// device) guard reuse.  The source may be freed as soon as this returns.
+// staging buffers are allocated once per process and shared by all devices;
+// each buffer is reused only after the copy that last read it (on whichever
+// device) has completed.  The source may be freed as soon as this returns.
 torch::Tensor upload(const torch::Tensor& t, torch::ScalarType dtype, const torch::Device& dev) {
     if (t.is_cuda()) return t.to(dev, dtype).contiguous();
     const torch::Tensor h = t.contiguous().to(dtype);
@@ -75,6 +76,7 @@ torch::Tensor upload(const torch::Tensor& t, torch::ScalarType dtype, const torc
     static std::mutex mu;
     static void* stage[2] = {nullptr, nullptr};
     static hipEvent_t done[64][2] = {};
+    static int last_dev[2] = {-1, -1};  // device whose copy last read each buffer
     std::lock_guard<std::mutex> lock(mu);
     const int di = dev.index();
     TORCH_CHECK(di >= 0 && di < 64, "upload: device index out of range");
@@ -91,13 +93,15 @@ torch::Tensor upload(const torch::Tensor& t, torch::ScalarType dtype, const torc
     int k = 0;
     for (int64_t off = 0; off < bytes; off += kStage, k ^= 1) {
         const int64_t len = std::min(kStage, bytes - off);
-        TORCH_CHECK(hipEventSynchronize(done[di][k]) == hipSuccess, "upload: staging wait failed");
+        if (last_dev[k] >= 0)
+            TORCH_CHECK(hipEventSynchronize(done[last_dev[k]][k]) == hipSuccess, "upload: staging wait failed");
         char* buf = static_cast<char*>(stage[k]);
         torch::from_blob(buf, {len}, torch::TensorOptions().dtype(torch::kUInt8))
             .copy_(torch::from_blob(const_cast<char*>(src) + off, {len}, torch::TensorOptions().dtype(torch::kUInt8)));
         TORCH_CHECK(hipMemcpyAsync(dst + off, buf, len, hipMemcpyHostToDevice, st) == hipSuccess,
                     "upload: copy failed");
         TORCH_CHECK(hipEventRecord(done[di][k], st) == hipSuccess, "upload: event record failed");
+        last_dev[k] = di;
     }
     return out;
 }
