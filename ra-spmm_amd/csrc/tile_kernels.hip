@@ -505,18 +505,20 @@ __global__ __launch_bounds__(kBlock) void tile_merge_kernel(
     const int32_t* __restrict__ win_rows, const float* __restrict__ scratch, float* __restrict__ C,
     int M, int N, int H, int cell_base, int accumulate) {
     const int sw = blockIdx.x;
-    const int64_t e = (int64_t)blockIdx.y * kBlock + threadIdx.x;
-    if (e >= (int64_t)H * N) return;
-    const int m = static_cast<int>(e / N);
-    const int n = static_cast<int>(e - (int64_t)m * N);
-    const int64_t slot_row = (int64_t)(split_windows[sw] - cell_base) * H + m;
-    const int row = win_rows ? win_rows[slot_row] : static_cast<int>(slot_row);
-    if (row < 0 || row >= M) return;
     const int o0 = split_offsets[sw], o1 = split_offsets[sw + 1];
-    float acc = scratch[((int64_t)o0 * H + m) * N + n];
-    for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * H + m) * N + n];
-    if (accumulate) acc = C[(int64_t)row * N + n] + acc;
-    C[(int64_t)row * N + n] = acc;
+    // grid.y is capped by the launch; stride over the window's H*N elements.
+    for (int64_t e = (int64_t)blockIdx.y * kBlock + threadIdx.x; e < (int64_t)H * N;
+         e += (int64_t)gridDim.y * kBlock) {
+        const int m = static_cast<int>(e / N);
+        const int n = static_cast<int>(e - (int64_t)m * N);
+        const int64_t slot_row = (int64_t)(split_windows[sw] - cell_base) * H + m;
+        const int row = win_rows ? win_rows[slot_row] : static_cast<int>(slot_row);
+        if (row < 0 || row >= M) continue;
+        float acc = scratch[((int64_t)o0 * H + m) * N + n];
+        for (int o = o0 + 1; o < o1; ++o) acc += scratch[((int64_t)o * H + m) * N + n];
+        if (accumulate) acc = C[(int64_t)row * N + n] + acc;
+        C[(int64_t)row * N + n] = acc;
+    }
 }
 
 // --------------------------------------------------------------- convert
@@ -668,7 +670,8 @@ ra_status launch_mfma_kind(const ra_tile_plan* p, const Part& part, const uint16
 ra_status launch_merge(const ra_tile_plan* p, const Part& part, float* C, int N, hipStream_t st) {
     if (part.num_splits == 0) return RA_OK;
     const int H = p->info.rows_per_window;
-    dim3 grid(part.num_splits, static_cast<unsigned>(((int64_t)H * N + kBlock - 1) / kBlock));
+    dim3 grid(part.num_splits,
+              static_cast<unsigned>(std::min<int64_t>(((int64_t)H * N + kBlock - 1) / kBlock, 65535)));
     const int32_t* wr = p->info.kind == RA_TILE_COMMUNITY_TC ? p->win_rows.get<int32_t>() : nullptr;
     tile_merge_kernel<<<grid, kBlock, 0, st>>>(p->split_windows.get<int32_t>() + part.split_base,
                                                p->split_offsets.get<int32_t>() + part.split_base, wr,
