@@ -4,7 +4,7 @@
   ZERO_OVERHEAD_CSR               rows <= 256 nnz bit-identical, all within 1e-5 of |A||B|
   tile FP16 route (any layout)    1e-5 of |Aq||Bq| against fp64 of the quantised inputs
   tile FP32 route (any layout)    1e-5 of |Aq||B| against fp64 of the stored values
-Shapes, densities, skew, empty rows, duplicate entries, N (1..300, ragged),
+Shapes, densities, skew, empty rows, duplicate entries, N (1..520, ragged),
 window heights, column partitions and the stored value type (fp16 / bf16)
 vary with the seed."""
 import os
@@ -39,11 +39,11 @@ def _graph(rng):
     return g
 
 
-@pytest.mark.parametrize("seed", range(48))
+@pytest.mark.parametrize("seed", range(64))
 def test_random_parity(oracle, seed):
     rng = np.random.default_rng(1000 + seed)
     g = _graph(rng)
-    N = int(rng.choice([1, 7, 16, 33, 64, 100, 128, 300]))
+    N = int(rng.choice([1, 7, 16, 33, 64, 100, 128, 260, 300, 512, 520]))
     print(f"[random] seed={seed} M={g.M} K={g.K} nnz={g.nnz} N={N}", flush=True)
     rp, ci, vl = g.torch("cuda")
     B = rng.standard_normal((g.K, N)).astype(np.float32)
