@@ -55,3 +55,6 @@ def test_block_of_carries_the_driver_fields():
     assert b["roofline"]["frac_of_gather_probe"] == round(0.81 / 0.9, 4)
     assert b["speedup_vs_rocsparse"] == 1.5 and b["rocsparse_alg"] == "csr_nnz_split"
     assert set(b["cold"]) == {"route_ms", "build_ms", "first_exec_ms"}
+    # a tile plan's probe walks its vector columns and is keyed plan_order
+    res["gather_ceiling"] = {"plan_order": {"ms": 0.45, "gathers": 10}}
+    assert bench.block_of(res)["roofline"]["frac_of_gather_probe"] == round(0.45 / 0.9, 4)
