@@ -522,13 +522,21 @@ LaneShape pick_shape(int np, int packet_elems, int slice_elems = 0) {
     return {G, V, U};
 }
 
+// True when grid.x * grid.y work-groups of kBlock lanes fit one grid dimension.
+inline bool fold_fits(dim3 grid) {
+    return static_cast<uint64_t>(grid.x) * grid.y * kBlock <= 0xFFFFFFFFull;
+}
+
 template <typename P>
 ra_status launch_csr_rows(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_t* rowptr,
                           const int32_t* colind, const float* vals, const P* B, P* C,
                           const int32_t* row_list, int64_t num_rows, int64_t ldp, int np, int resume) {
     const int remap = tuning().remap, nt = tuning().nt;
     int nslices = 0;
-    if (tuning().xslice && grid.y > 1) {
+    // Folding the column slices into grid.x is legal only while the folded
+    // grid stays below 2^32 work-items (grid.x * blockDim on AMD); beyond
+    // that the 2-D grid (one slice per grid.y) is kept.
+    if (tuning().xslice && grid.y > 1 && fold_fits(grid)) {
         nslices = static_cast<int>(grid.y);
         grid = dim3(grid.x * grid.y, 1);
     }
@@ -564,7 +572,7 @@ ra_status launch_zo(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_
                     bool xcd_slices) {
     const int remap = tuning().zo_remap, nt = tuning().nt, sole_split = tuning().sole_split;
     int nslices = 0;
-    if (xcd_slices && grid.y > 1) {
+    if (xcd_slices && grid.y > 1 && fold_fits(grid)) {  // same 2^32 work-item bound
         nslices = static_cast<int>(grid.y);
         grid = dim3(grid.x * grid.y, 1);
     }

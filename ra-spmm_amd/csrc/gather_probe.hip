@@ -60,8 +60,14 @@ extern "C" {
 // Gathers B[idx[i], 0:4*packets] for i < n.  B: fp32, row stride ldp float4
 // packets; packets in {4, 8, 16, 32, 64} (N = 16..256 columns); each lane
 // group walks `span` consecutive indices.  out must hold
-// ra_probe_out_elems(n, packets, span) float4.  Returns 0, or -1 on bad arguments.
+// ra_probe_out_elems(n, packets, span) float4 (that function returns -1 for
+// packets or span out of range).  Returns 0, or -1 on bad arguments.
+static bool probe_args_ok(int32_t packets, int32_t span) {
+    return (packets == 4 || packets == 8 || packets == 16 || packets == 32 || packets == 64) && span >= 1;
+}
+
 int64_t ra_probe_out_elems(int64_t n, int32_t packets, int32_t span) {
+    if (!probe_args_ok(packets, span)) return -1;
     const int64_t groups = (n + span - 1) / span;
     const int64_t rpw = kWave / packets;
     const int64_t waves = (groups + rpw - 1) / rpw;
@@ -70,8 +76,8 @@ int64_t ra_probe_out_elems(int64_t n, int32_t packets, int32_t span) {
 
 int ra_probe_gather(const float* B, int64_t ldp, int32_t packets, const int32_t* idx, int64_t n, int32_t span,
                     float* out, void* stream) {
+    if (!probe_args_ok(packets, span)) return -1;
     if (n <= 0) return 0;
-    if (span < 1) return -1;
     const int64_t blocks = ra_probe_out_elems(n, packets, span) / kBlock;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const float4* B4 = reinterpret_cast<const float4*>(B);

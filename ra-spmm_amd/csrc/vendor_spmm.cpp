@@ -85,8 +85,13 @@ int ra_vendor_spmm_create(const int32_t* d_rowptr, const int32_t* d_colind, cons
     return 0;
 }
 
-int ra_vendor_spmm_run(void* plan) {
-    const rocsparse_status s = spmm(static_cast<VendorPlan*>(plan), rocsparse_spmm_stage_compute);
+// Runs on `stream` (the caller's current stream at this call, so C is written
+// in order with the work that allocates and reads it).
+int ra_vendor_spmm_run(void* plan, void* stream) {
+    auto* p = static_cast<VendorPlan*>(plan);
+    rocsparse_status s = rocsparse_set_stream(p->handle, static_cast<hipStream_t>(stream));
+    if (s != rocsparse_status_success) return fail("rocsparse set stream", s);
+    s = spmm(p, rocsparse_spmm_stage_compute);
     return s == rocsparse_status_success ? 0 : fail("rocsparse compute", s);
 }
 

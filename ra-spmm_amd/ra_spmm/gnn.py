@@ -51,6 +51,8 @@ def build_aggregation_operator(csr, model: str):
                   absent, and deg~ its row sums (rows of zero degree stay 0)
     sage          W[i, j] = a_ij / deg_i (row mean; empty rows stay zero)
     gin           W = A
+    The gcn and sage operators store no zero entries (the reference forms
+    them as sparse products, which drop zeros); gin keeps A's structure.
     Duplicate entries of A are summed first.  The matrix is built once, so
     every backend and the correctness reference consume the same operator
     (gnn_bench/router_vs_baselines_gcn.py:89-126)."""
@@ -79,6 +81,7 @@ def build_aggregation_operator(csr, model: str):
         tilde.sort_indices()
         norm = reciprocal(np.asarray(tilde.sum(axis=1)).ravel(), 0.5)
         tilde.data = tilde.data * (norm[row_of_entry(tilde)] * norm[tilde.indices])
+        tilde.eliminate_zeros()  # the product D A D stores no zero entries
         weights = tilde
     elif kind == "gin":
         weights = adj
@@ -86,6 +89,7 @@ def build_aggregation_operator(csr, model: str):
         inv_deg = reciprocal(np.asarray(adj.sum(axis=1)).ravel(), 1.0)
         weights = adj.copy()
         weights.data = weights.data * inv_deg[row_of_entry(weights)]
+        weights.eliminate_zeros()  # the product D^-1 A stores no zero entries
     out = sp.csr_matrix(weights, dtype=np.float32)
     out.sort_indices()
     return out

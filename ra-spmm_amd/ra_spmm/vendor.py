@@ -26,7 +26,7 @@ def _lib():
         I32, I64 = ctypes.c_int32, ctypes.c_int64
         lib.ra_vendor_spmm_create.argtypes = [P, P, P, P, P, I32, I32, I32, I64, I32, P, ctypes.POINTER(P)]
         lib.ra_vendor_spmm_create.restype = ctypes.c_int
-        lib.ra_vendor_spmm_run.argtypes = [P]
+        lib.ra_vendor_spmm_run.argtypes = [P, P]
         lib.ra_vendor_spmm_run.restype = ctypes.c_int
         lib.ra_vendor_spmm_set_dense.argtypes = [P, P, P]
         lib.ra_vendor_spmm_set_dense.restype = ctypes.c_int
@@ -73,7 +73,8 @@ class RocsparseSpMM:
         self._keep = old[:3] + (B, C)
 
     def run(self):
-        st = _lib().ra_vendor_spmm_run(self._h)
+        # The current stream of this call, not the one current at creation.
+        st = _lib().ra_vendor_spmm_run(self._h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         if st != 0:
             raise RuntimeError(f"rocsparse: {_lib().ra_vendor_last_error().decode()}")
         return self._keep[4]

@@ -107,3 +107,11 @@ def test_gcn_operator_self_loops_and_duplicates():
     sage = build_aggregation_operator(A, "sage").toarray()
     rs = dense.sum(1)
     np.testing.assert_allclose(sage[rs > 0], (dense / np.where(rs > 0, rs, 1)[:, None])[rs > 0], rtol=1e-6)
+
+    # Stored zeros are dropped from the products (sparse D^-1 A keeps none):
+    # the structure is exactly the nonzero pattern of the dense result.
+    sage_csr = build_aggregation_operator(A, "sage")
+    assert sage_csr.nnz == int(np.count_nonzero(sage)) == 5
+    assert op.nnz == int(np.count_nonzero(op.toarray()))
+    gin = build_aggregation_operator(A, "gin")
+    assert gin.nnz == 6  # duplicates summed, the stored zero kept
