@@ -486,8 +486,10 @@ def block_of(res):
     cpu = res.get("cpu_torch_sparse") or {}
     b = {
         "path": res["path"], "ms": round(res["ms_per_step"], 5), "gflops": round(res["gflops"], 2),
+        # kernel_ms and bytes_alg are per SpMM call: every launch of the kernel
+        # in one call (one per column partition of a tile plan)
         "roofline": {"kernel": res["kernel"], "kernel_ms": round(res["kernel_ms"], 5),
-                     "bytes_alg": res["bytes_alg"], "frac": round(frac, 4)},
+                     "bytes_alg": res["bytes_alg"], "frac": round(frac, 4), "per": "call"},
         "cold": {"route_ms": round(res["cold_route_ms"], 4), "build_ms": round(res["cold_build_ms"], 3),
                  "first_exec_ms": round(res["cold_first_exec_ms"], 4)},
         "baseline_kernel_ms": round(res["baseline_ms"], 5),
@@ -592,6 +594,14 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
     torch.cuda.synchronize()
     del warm, wopt
     for backend in backends:
+        # Every backend is validated on this operator before it is timed, as
+        # the reference does (gnn_bench/router_vs_baselines_gcn.py:413-446,
+        # 566-567): each (transpose, N) SpMM of the step, N = 256 and 47,
+        # against the baseline kernel with the harness's gate.
+        val = gnn.validate_backend(op, "cuda", backend, (256, 47), seed=0, table=table)
+        torch.cuda.empty_cache()
+        log(f"[gcn] {backend:14s} validation: correct={val['correct']} max_error={val['max_error']:.3e} "
+            f"tolerance={val['tolerance']:.3e}")
         torch.manual_seed(1)
         graph = gnn.GraphBackend(op, "cuda", table)
         model = gnn.GCN(128, 256, 47).cuda()
@@ -603,7 +613,8 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
             gnn.train_step(model, graph, backend, X, y, opt)
         ts = [gnn.train_step(model, graph, backend, X, y, opt) for _ in range(steps)]
         ms = 1e3 * sum(ts) / len(ts)
-        rec = {"step_ms": ms, "cold_first_step_ms": cold * 1e3}
+        rec = {"step_ms": ms, "cold_first_step_ms": cold * 1e3,
+               "validation": {k: val[k] for k in ("correct", "max_error", "tolerance")}}
         if backend == "router":
             rec["paths"] = {f"{'bwd' if t else 'fwd'}_N{n}": lab
                             for (b, t, n), (lab, _) in graph.exec_cache.items()}
@@ -638,12 +649,17 @@ def sweep(configs, Ns, steps, out_path):
     import torch
     import ra_spmm
     from ra_spmm import synthetic as S
+    from ra_spmm.router import production_features
     rows = []
     for cfg in configs:
         S.use_device_sort("cuda")
-        g = S.CONFIGS[cfg]()
+        g = S.CONFIGS[cfg]() if cfg in S.CONFIGS else S.REGIMES[cfg]()
+        feat = production_features(g.rowptr)
         rp, ci, vl = g.torch("cuda")
         host = (rp.cpu(), ci.cpu(), vl.cpu())  # plan builders take host CSR, as in the reference
+        gdesc = {"M": g.M, "nnz": g.nnz, "d": feat["avg_nnz_per_row"], "cv": feat["degree_cv"],
+                 "max_deg": feat["max_deg"]}
+        log(f"[sweep] {cfg}: M={g.M} nnz={g.nnz} d={gdesc['d']:.3f} cv={gdesc['cv']:.4f}")
         for N in Ns:
             B = torch.randn(g.K, N, device="cuda")
             base = ra_spmm.spmm_csr_baseline(rp, ci, vl, B)
@@ -653,7 +669,7 @@ def sweep(configs, Ns, steps, out_path):
             if roc.get("ms"):
                 rows.append({"config": cfg, "N": N, "path": "ROCSPARSE", "ms": roc["ms"],
                              "gflops": 2.0 * g.nnz * N / (roc["ms"] * 1e-3) / 1e9, "alg": roc["alg"],
-                             "routed": False})
+                             "routed": False, **gdesc})
                 log(f"[sweep] {cfg} N={N:4d} {'ROCSPARSE':22s} {roc['ms']:9.3f} ms ({roc['alg']})")
             for label in ["CSR_BASELINE"] + ra_spmm.DEPLOYED_KERNELS:
                 if label in ra_spmm.TILE_KERNELS and N < 16:
@@ -664,13 +680,22 @@ def sweep(configs, Ns, steps, out_path):
                 build = (time.perf_counter() - t) * 1e3
                 fn = lambda: ra_spmm.run_planned_kernel(label, plan, rp, ci, vl, B)  # noqa: E731
                 wall, ev = timed_steps(fn, steps, 3)
-                err = float(((fn() - base).abs() / (scale + 1e-30)).max())
+                out = fn()
+                err = float(((out - base).abs() / (scale + 1e-30)).max())
+                # The harness's gate (absolute, 1e-3 sqrt(max row nnz), x10 for the
+                # tile paths): the elementwise relative error of a 16-bit path is
+                # 1 wherever a B entry rounds to zero in a one-term row.
+                gate = ra_spmm.correctness_gate(label, float((out - base).abs().max()),
+                                                gdesc["max_deg"])
+                del out
                 row = {"config": cfg, "N": N, "path": label, "ms": wall, "event_ms": ev,
                        "gflops": 2.0 * g.nnz * N / (wall * 1e-3) / 1e9, "build_ms": build,
-                       "max_rel_err_vs_baseline": err, "routed": label == routed}
+                       "max_rel_err_vs_baseline": err, "max_abs_err": gate["max_error"],
+                       "gate_ok": gate["correct"], "routed": label == routed, **gdesc}
                 rows.append(row)
                 log(f"[sweep] {cfg} N={N:4d} {label:22s} {wall:9.3f} ms {row['gflops']:9.1f} GF/s "
-                    f"build {build:8.1f} ms err {err:.2e}")
+                    f"build {build:8.1f} ms err {err:.2e} abs {gate['max_error']:.2e} "
+                    f"{'ok' if gate['correct'] else 'GATE-FAIL'}")
                 if label in ("TC_DIRECT", "COMMUNITY_TC", "SEGMENT_HYBRID") and cfg in ("C3", "C4") \
                         and N % 8 == 0:
                     # fp16-B configs: the native 16-bit-B entry, no conversion pass
@@ -680,7 +705,7 @@ def sweep(configs, Ns, steps, out_path):
                     err16 = float(((f16() - base).abs() / (scale + 1e-30)).max())
                     rows.append({"config": cfg, "N": N, "path": label + "+B16", "ms": w16, "event_ms": e16,
                                  "gflops": 2.0 * g.nnz * N / (w16 * 1e-3) / 1e9, "build_ms": build,
-                                 "max_rel_err_vs_baseline": err16, "routed": False})
+                                 "max_rel_err_vs_baseline": err16, "routed": False, **gdesc})
                     log(f"[sweep] {cfg} N={N:4d} {label + '+B16':22s} {w16:9.3f} ms "
                         f"{rows[-1]['gflops']:9.1f} GF/s err {err16:.2e}")
                     del B16
@@ -688,6 +713,9 @@ def sweep(configs, Ns, steps, out_path):
             del B
         del rp, ci, vl, host
         torch.cuda.empty_cache()
+        if out_path:  # after every graph, so a cut-off run keeps what it measured
+            Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+            Path(out_path).write_text(json.dumps(rows, indent=1))
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)
         Path(out_path).write_text(json.dumps(rows, indent=1))
@@ -715,7 +743,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--traffic", type=float, default=None,
                     help="HBM bytes per launch of the dominant kernel from rocprofv3 --pmc")
-    ap.add_argument("--sweep", default=None, help="comma-separated configs to sweep all paths on")
+    ap.add_argument("--sweep", default=None, help="comma-separated configs (C1..C5, regime names, or 'regimes' for the "
+                         "router calibration suite) to sweep all paths on")
     ap.add_argument("--sweep-N", default="64,128,256")
     ap.add_argument("--sweep-out", default=None, help="write the sweep rows here as JSON")
     ap.add_argument("--details", default=None, help="write the full result dict here")
@@ -747,7 +776,14 @@ def main(argv=None):
         gather_sweep(args.details)
         return 0
     if args.sweep:
-        sweep(args.sweep.split(","), [int(n) for n in args.sweep_N.split(",")], max(10, args.steps // 4),
+        names = []
+        for n in args.sweep.split(","):
+            if n == "regimes":  # the router calibration suite
+                from ra_spmm import synthetic as S
+                names += list(S.REGIMES)
+            else:
+                names.append(n)
+        sweep(names, [int(n) for n in args.sweep_N.split(",")], max(10, args.steps // 4),
               args.sweep_out)
         return 0
 
@@ -772,11 +808,15 @@ def main(argv=None):
                "router_cold_first_step_ms": round(g5["router"]["cold_first_step_ms"], 2),
                "router_paths": g5["router"]["paths"],
                "rocsparse_step_ms": round(g5["rocsparse"]["step_ms"], 3),
-               "speedup_vs_rocsparse": round(g5["rocsparse"]["step_ms"] / g5["router"]["step_ms"], 3)}
+               "speedup_vs_rocsparse": round(g5["rocsparse"]["step_ms"] / g5["router"]["step_ms"], 3),
+               # each backend checked at full size before it was timed
+               "router_validation": g5["router"]["validation"],
+               "rocsparse_validation": g5["rocsparse"]["validation"]}
     achieved = res["bytes_alg"] / (res["kernel_ms"] * 1e-3) / 1e9
     copy_gbs = hbm_copy_gbs()
     traffic = args.traffic if args.traffic is not None else profile_traffic(res["kernel"], cfg, res["N"])
     l2_miss_gbs = traffic / (res["kernel_ms"] * 1e-3) / 1e9 if traffic else None
+    gather_ms = next(iter(res["gather_ceiling"].values()))["ms"] if res.get("gather_ceiling") else None
     line = {
         "metric": METRIC, "value": round(res["gflops"], 3), "unit": "GFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 5),
@@ -787,7 +827,16 @@ def main(argv=None):
                    "N": res["N"], "router_table": args.table},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": res["kernel"],
+                     # the north star's bar for the CSR regimes, and the fraction a
+                     # kernel running at the gather probe's time would reach: the
+                     # gap between frac and target_frac is not closed
+                     "target_frac": 0.6,
+                     "gather_ceiling_ms": round(gather_ms, 5) if gather_ms else None,
+                     "frac_at_gather_ceiling": round(res["bytes_alg"] / (gather_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+                     if gather_ms else None,
+                     # bytes per launch of the named kernel (the path is one launch
+                     # of it per SpMM call)
+                     "traffic": traffic, "traffic_unit": "bytes per launch", "kernel": res["kernel"],
                      "kernel_ms": round(res["kernel_ms"], 5), "bytes_alg": res["bytes_alg"],
                      # rocprofv3 FETCH_SIZE + WRITE_SIZE per launch counts the L2's
                      # requests to the fabric, which the 256 MB Infinity Cache (MALL)

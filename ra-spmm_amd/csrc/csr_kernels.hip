@@ -486,11 +486,13 @@ struct LaneShape {
 // slowest dimension), so each pass gathers only a c-column slice of B;
 // RA_ZO_SOLE_SPLIT=1 splits sole ZO chunks over the wave's lane groups;
 // RA_ZO_LDS_STAGE=0 turns off the LDS staging of the chunks' (column, value)
-// pairs.
+// pairs; RA_CSR_SLICE=c sets CSR_DIRECT's XCD-dealt column slice (0 off;
+// default 128 columns at N >= 256 when the unsliced grid has < 2^16 waves).
 struct CsrTuning {
     int lanes = 0, unroll = 4, remap = 1, zo_remap = 0, nt = 1, coltile = 0, sole_split = 0, xslice = 0,
-        zo_slice = -1, lds_stage = 1;
+        zo_slice = -1, lds_stage = 1, csr_slice = -1;
     CsrTuning() {
+        if (const char* e = std::getenv("RA_CSR_SLICE")) csr_slice = std::atoi(e);
         if (const char* e = std::getenv("RA_ZO_LDS_STAGE")) lds_stage = std::atoi(e) != 0;
         if (const char* e = std::getenv("RA_ZO_SLICE")) zo_slice = std::atoi(e);
         if (const char* e = std::getenv("RA_CSR_XSLICE")) xslice = std::atoi(e) != 0;
@@ -530,13 +532,14 @@ inline bool fold_fits(dim3 grid) {
 template <typename P>
 ra_status launch_csr_rows(const LaneShape& sh, dim3 grid, hipStream_t st, const int32_t* rowptr,
                           const int32_t* colind, const float* vals, const P* B, P* C,
-                          const int32_t* row_list, int64_t num_rows, int64_t ldp, int np, int resume) {
+                          const int32_t* row_list, int64_t num_rows, int64_t ldp, int np, int resume,
+                          bool xcd_slices) {
     const int remap = tuning().remap, nt = tuning().nt;
     int nslices = 0;
     // Folding the column slices into grid.x is legal only while the folded
     // grid stays below 2^32 work-items (grid.x * blockDim on AMD); beyond
     // that the 2-D grid (one slice per grid.y) is kept.
-    if (tuning().xslice && grid.y > 1 && fold_fits(grid)) {
+    if (xcd_slices && grid.y > 1 && fold_fits(grid)) {
         nslices = static_cast<int>(grid.y);
         grid = dim3(grid.x * grid.y, 1);
     }
@@ -626,15 +629,28 @@ ra_status csr_direct_launch(const int32_t* d_rowptr, const int32_t* d_colind, co
     if (M == 0 || N == 0) return RA_OK;
     const bool vec = (N % 4 == 0) && ra::aligned16(d_B) && ra::aligned16(d_C);
     const int np = vec ? N / 4 : N;
-    const LaneShape sh = pick_shape(np, vec ? 4 : 1);
+    // Wide rows of a small matrix: 128-column slices dealt to the XCDs, as
+    // ZERO_OVERHEAD_CSR does, so that fewer than 2^16 waves (about 64 per CU)
+    // become 2-4x as many, each with a shorter chain of dependent gathers.
+    // On larger matrices the slices only re-read A per slice (config 3 at
+    // N=512: 1.91 -> 2.18 ms), so they stay off there.
+    int cslice = tuning().csr_slice;
+    if (cslice < 0) {
+        const LaneShape whole = pick_shape(np, vec ? 4 : 1);
+        const int64_t waves = (static_cast<int64_t>(M) + kWave / whole.G - 1) / (kWave / whole.G);
+        cslice = (vec && N >= 256 && waves < (int64_t{1} << 16)) ? 128 : 0;
+    }
+    const LaneShape sh = pick_shape(np, vec ? 4 : 1, cslice);
+    const bool deal = cslice > 0 || tuning().xslice;
     const int rows_per_block = kWavesPerBlock * (kWave / sh.G);
     dim3 grid((M + rows_per_block - 1) / rows_per_block, (np + sh.G * sh.V - 1) / (sh.G * sh.V));
     if (vec)
         return launch_csr_rows<float4>(sh, grid, st, d_rowptr, d_colind, d_vals,
                                        reinterpret_cast<const float4*>(d_B),
-                                       reinterpret_cast<float4*>(d_C), nullptr, M, np, np, resume ? 1 : 0);
+                                       reinterpret_cast<float4*>(d_C), nullptr, M, np, np, resume ? 1 : 0,
+                                       deal);
     return launch_csr_rows<float>(sh, grid, st, d_rowptr, d_colind, d_vals, d_B, d_C,
-                                  nullptr, M, np, np, resume ? 1 : 0);
+                                  nullptr, M, np, np, resume ? 1 : 0, deal);
 }
 
 }  // namespace ra

@@ -45,40 +45,53 @@ struct RouterTable {
     float d_fp32_small;      //       d <)
     // MI355X-only knobs (inert in the reference table).
     int   fp32_route_csr;    // FP32-route picks go to the CSR family instead
-    int   skewed_to_zo;      // rule 3 sends skewed graphs to ZERO_OVERHEAD_CSR
     float zo_min_cv;         // CSR_DIRECT picks with cv >= this go to ZERO_OVERHEAD_CSR
     int   n_uniform_csr;     // rule 2, remaining uniform graphs: N <= -> CSR_DIRECT
+    int   skewed_path;       // rule 3: path, or -1 for the split on M
+    int   small_dense_path;  // rule 5: path, or -1 for the split on N
+    int   heavy_path;        // rule 6 path
+    int   web_path;          // rule 7 path
+    int   web_fp32;          //   rule 7 forces the FP32 route
+    float fp32_small_max_cv; // the small-graph FP32 condition applies only when cv <
 };
 
 // Published thresholds (router/router_dispatch.cpp:1004-1094, ra_router_eval.py:37-124).
 constexpr RouterTable kReference = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 2e-8, 20.0, 5.0f, 25000, 9.0f,
-    0, 0, 1e30f, 0};
+    0, 1e30f, 0, -1, -1, RA_PATH_COMMUNITY_TC, RA_PATH_COMMUNITY_TC, 1, 1e30f};
 
-// MI355X calibration (structure of the tree unchanged; measured on gfx950 with
-// bench.py --sweep over the five benchmark configs C1-C5):
-//  - tile gate: the device tile build (sorts and scans on the GPU) runs at
-//    1.0-1.9e-10 s per nnz (C2 1.6e7 nnz: 2.8 ms; C4 1.24e8 nnz: 12.7 ms),
-//    plus ~3e-10 s per nnz to upload a host CSR (the host builder took
-//    0.75-1.5e-8 s per nnz), so the estimate is 1e-9 s per nnz with the same
-//    20 s budget;
-//  - FP32-route tile picks go to the CSR family, which needs no plan: the FP32
-//    tile route runs the same CSR kernels on the plan's stored values, after a
-//    tile build (C1: 3.3 ms) and a one-time derivation of that CSR;
-//  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR:
-//    one lane group per hub row is 6.6x slower on config 2.
-//  - rule 2's remaining uniform graphs at N <= 64 go to CSR_DIRECT: at 64
-//    columns the MFMA kernel gathers 8 bytes per lane, and on config 3 CSR_DIRECT
-//    takes 0.210 ms against 0.240 ms for TC_DIRECT (0.49 vs 0.37 ms at N=128).
-//  Rules 1-7 otherwise keep the published thresholds: COMMUNITY_TC for
-//  dense/heavy rows (config 4: 16.5 ms, the fastest path), TC_DIRECT for the
-//  uniform family (config 3), ZERO_OVERHEAD_CSR for extreme skew (the fp32
-//  path on configs 2 and 5).
+// MI355X calibration.  The structure of the tree is unchanged; each knob is
+// set from one measured sweep on gfx950 (bench.py --sweep regimes,C1,...,C5
+// at N = 64, 128, 256, 512: 27 graphs, 108 points, at least one graph in every
+// branch of the tree; router_eval.py scores a table against it):
+//  - tile gate: the device tile build runs at 1.0-1.9e-10 s per nnz, plus
+//    ~3e-10 s per nnz to upload a host CSR, so the estimate is 1e-9 s per nnz
+//    with the same 20 s budget;
+//  - FP32-route tile picks go to the CSR family, which needs no plan (the
+//    FP32 tile route runs the same CSR kernels on the plan's stored values);
+//  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR
+//    (one lane group per hub row is 6.6x slower on config 2);
+//  - rule 2, uniform graphs of d >= 7 at N <= 64 go to CSR_DIRECT (config 3
+//    0.212 vs 0.218 ms for TC_DIRECT);
+//  - rules 3, 5 and 6 pick SEGMENT_HYBRID: the fastest path on 25 of the 32
+//    points of those regions and within 12% on the rest (rule 5's guardrail
+//    pick, the baseline kernel, was 4-6x slower; rule 6's COMMUNITY_TC 1.5x
+//    slower on a graph with local columns; rule 3's split on M gave
+//    COMMUNITY_TC to large graphs, where it was 0-40% slower);
+//  - rule 7 picks TC_DIRECT without forcing the FP32 route (fastest on 5 of
+//    8 points; COMMUNITY_TC on the FP32 route meant CSR_DIRECT here, 1.4x
+//    slower at N = 64-128), and the small-graph FP32 condition (M <= 25000,
+//    d < 9) holds only for uniform rows (cv < 0.7): on a small graph of cv 1
+//    the 16-bit tiles beat the CSR kernels 1.4-1.9x.
+//  Rule 1 keeps ZERO_OVERHEAD_CSR, the exact fp32 path, although the fp16
+//  COMMUNITY_TC is 1.4-1.7x faster on configs 2 and 5: the router does not
+//  trade precision for speed on extreme skew.
 constexpr RouterTable kMI355X = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-9, 20.0, 5.0f, 25000, 9.0f,
-    1, 0, 1.5f, 64};
+    1, 1.5f, 64, RA_PATH_SEGMENT_HYBRID, RA_PATH_SEGMENT_HYBRID, RA_PATH_SEGMENT_HYBRID,
+    RA_PATH_TC_DIRECT, 0, 0.7f};
 
 bool tile_family(int p) {
     return p == RA_PATH_TC_DIRECT || p == RA_PATH_COMMUNITY_TC || p == RA_PATH_SEGMENT_HYBRID;
@@ -238,7 +251,8 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
     auto pick_tile = [&](int p, const char* why, bool force_fp32) {
         if (tile_ok && out->feasible[p]) {
             const bool want_fp32 =
-                force_fp32 || (d < T.d_fp32_route || (M <= T.m_fp32_small && d < T.d_fp32_small));
+                force_fp32 || (d < T.d_fp32_route || (M <= T.m_fp32_small && d < T.d_fp32_small &&
+                                                      cv < T.fp32_small_max_cv));
             if (want_fp32 && T.fp32_route_csr) {
                 csr_by_skew("csr_direct_over_fp32_tile", "zero_overhead_over_fp32_tile");
                 return;
@@ -249,6 +263,18 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
             fp32_route = want_fp32;
         } else {
             csr_by_skew("csr_direct_tile_gated", "zero_overhead_tile_gated");
+        }
+    };
+
+    // A rule's path from the table: a tile family goes through the tile gate
+    // and the precision rule, a CSR family is taken as is.
+    auto pick_table = [&](int p, const char* why) {
+        if (tile_family(p)) {
+            pick_tile(p, why, false);
+        } else {
+            choice = p;
+            reason = why;
+            risk = p == RA_PATH_ZERO_OVERHEAD_CSR ? 0.06f : 0.05f;
         }
     };
 
@@ -284,10 +310,8 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
         }
     } else if (cv >= T.cv_skewed) {
         rule = 3;
-        if (T.skewed_to_zo) {
-            choice = RA_PATH_ZERO_OVERHEAD_CSR;
-            reason = "zero_overhead_skewed";
-            risk = 0.06f;
+        if (T.skewed_path >= 0) {
+            pick_table(T.skewed_path, "segment_hybrid_skewed");
         } else if (M >= T.m_skewed_large) {
             pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_skewed_large", false);
         } else {
@@ -298,7 +322,9 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
         pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_dense_rows", false);
     } else if (M < T.m_small && d >= T.d_small_dense) {
         rule = 5;
-        if (N < T.n_small_narrow) {
+        if (T.small_dense_path >= 0) {
+            pick_table(T.small_dense_path, "segment_hybrid_small_dense_allN");
+        } else if (N < T.n_small_narrow) {
             choice = RA_PATH_CUSPARSE;
             reason = "cusparse_small_dense_narrowN";
             risk = 0.05f;
@@ -309,10 +335,14 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
         }
     } else if (d >= T.d_heavy && cv >= T.cv_heavy) {
         rule = 6;
-        pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_heavy_mixed", false);
+        pick_tile(T.heavy_path, T.heavy_path == RA_PATH_COMMUNITY_TC ? "community_tc_heavy_mixed"
+                                                                     : "segment_hybrid_heavy_mixed",
+                  false);
     } else if (d < T.d_web && cv >= T.cv_web_lo && cv <= T.cv_web_hi && M >= T.m_web) {
         rule = 7;
-        pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_web_locality", true);
+        pick_tile(T.web_path, T.web_path == RA_PATH_COMMUNITY_TC ? "community_tc_web_locality"
+                                                                 : "tc_direct_web_locality",
+                  T.web_fp32 != 0);
     } else {
         rule = 8;
         pick_tile(RA_PATH_TC_DIRECT, "tc_direct_default", false);

@@ -65,15 +65,22 @@ class RouterTable:
     m_fp32_small: int = 25000
     d_fp32_small: float = 9.0
     fp32_route_csr: bool = False
-    skewed_to_zo: bool = False
     zo_min_cv: float = 1e30
     n_uniform_csr: int = 0
+    skewed_path: str | None = None       # rule 3: None = reference split on M
+    small_dense_path: str | None = None  # rule 5: None = reference split on N
+    heavy_path: str = "COMMUNITY_TC"     # rule 6
+    web_path: str = "COMMUNITY_TC"       # rule 7
+    web_fp32: bool = True                #   rule 7 forces the FP32 route
+    fp32_small_max_cv: float = 1e30      # small-graph FP32 condition only when cv <
 
 
 REFERENCE = RouterTable()
 # Calibrated on gfx950 (values and measurements: csrc/router.cpp, kMI355X).
-MI355X = RouterTable(plan_s_per_nnz=1e-9, fp32_route_csr=True, skewed_to_zo=False, zo_min_cv=1.5,
-                     n_uniform_csr=64)
+MI355X = RouterTable(plan_s_per_nnz=1e-9, fp32_route_csr=True, zo_min_cv=1.5, n_uniform_csr=64,
+                     skewed_path="SEGMENT_HYBRID", small_dense_path="SEGMENT_HYBRID",
+                     heavy_path="SEGMENT_HYBRID", web_path="TC_DIRECT", web_fp32=False,
+                     fp32_small_max_cv=0.7)
 TABLES = {"reference": REFERENCE, "mi355x": MI355X}
 
 
@@ -158,10 +165,16 @@ def route_with_rules(avg_nnz, degree_cv, M, N, nnz=None, *, disabled_rules=(), t
     def csr_by_skew():
         return "CSR_DIRECT" if cv < _f32(T.cv_gate_csr) else "ZERO_OVERHEAD_CSR"
 
+    def _direct(path):
+        # A rule's path from the table: a tile family goes through the tile
+        # gate and the precision rule, a CSR family is taken as is.
+        return pick(path) if path in ("TC_DIRECT", "COMMUNITY_TC", "SEGMENT_HYBRID") else (path, False)
+
     def pick(kernel, force_fp32=False):
         if tile_ok:
             want = force_fp32 or (d < _f32(T.d_fp32_route)
-                                  or (M <= T.m_fp32_small and d < _f32(T.d_fp32_small)))
+                                  or (M <= T.m_fp32_small and d < _f32(T.d_fp32_small)
+                                      and cv < _f32(T.fp32_small_max_cv)))
             if want and T.fp32_route_csr:
                 return csr_by_skew(), False
             return kernel, want
@@ -179,8 +192,8 @@ def route_with_rules(avg_nnz, degree_cv, M, N, nnz=None, *, disabled_rules=(), t
         else:
             choice, fp32 = pick("TC_DIRECT")
     elif 3 not in disabled and cv >= _f32(T.cv_skewed):
-        if T.skewed_to_zo:
-            choice = "ZERO_OVERHEAD_CSR"
+        if T.skewed_path is not None:
+            choice, fp32 = _direct(T.skewed_path)
         elif M >= T.m_skewed_large:
             choice, fp32 = pick("COMMUNITY_TC")
         else:
@@ -188,17 +201,19 @@ def route_with_rules(avg_nnz, degree_cv, M, N, nnz=None, *, disabled_rules=(), t
     elif 4 not in disabled and d >= _f32(T.d_dense):
         choice, fp32 = pick("COMMUNITY_TC")
     elif 5 not in disabled and M < T.m_small and d >= _f32(T.d_small_dense):
-        if N < T.n_small_narrow:
+        if T.small_dense_path is not None:
+            choice, fp32 = _direct(T.small_dense_path)
+        elif N < T.n_small_narrow:
             choice = "CUSPARSE"
         elif N < T.n_small_mid:
             choice, fp32 = pick("SEGMENT_HYBRID")
         else:
             choice, fp32 = pick("COMMUNITY_TC")
     elif 6 not in disabled and d >= _f32(T.d_heavy) and cv >= _f32(T.cv_heavy):
-        choice, fp32 = pick("COMMUNITY_TC")
+        choice, fp32 = pick(T.heavy_path)
     elif (7 not in disabled and d < _f32(T.d_web) and cv >= _f32(T.cv_web_lo)
           and cv <= _f32(T.cv_web_hi) and M >= T.m_web):
-        choice, fp32 = pick("COMMUNITY_TC", True)
+        choice, fp32 = pick(T.web_path, T.web_fp32)
     else:
         choice, fp32 = pick("TC_DIRECT")
 

@@ -243,6 +243,88 @@ def random_csr(M: int, K: int, avg_deg: float, seed: int = 0, skew: float = 0.0,
     return Graph(rowptr.astype(np.int32), cols, vals, M, K, f"random_{M}x{K}")
 
 
+def degree_sequence(rng, M: int, avg_deg: float, cv: float, max_deg: int) -> np.ndarray:
+    """Row lengths with mean ~avg_deg and population CV ~cv, clipped to
+    [1, max_deg].  cv < 0.7: gamma-Poisson mixture (CV^2 = 1/k + 1/avg);
+    otherwise log-normal with sigma^2 = ln(1 + cv^2), rescaled after clipping."""
+    if cv * cv <= 1.0 / avg_deg:
+        deg = rng.poisson(avg_deg, size=M)
+    elif cv < 0.7:
+        k = 1.0 / (cv * cv - 1.0 / avg_deg)
+        deg = rng.poisson(rng.gamma(k, avg_deg / k, size=M))
+    else:
+        sigma = float(np.sqrt(np.log1p(cv * cv)))
+        z = rng.standard_normal(M)
+        scale = avg_deg
+        for _ in range(30):  # mean after clipping and rounding -> avg_deg
+            raw = np.exp(sigma * z - sigma * sigma / 2.0) * scale
+            deg = np.clip(np.rint(raw), 1, max_deg)
+            scale *= avg_deg / max(deg.mean(), 1e-9)
+    return np.clip(deg, 1, max_deg).astype(np.int64)
+
+
+def regime_graph(M: int, avg_deg: float, cv: float, locality: float = 0.0, window: int = 256,
+                 popular: bool = False, seed: int = 0, max_deg: int | None = None,
+                 name: str = "") -> Graph:
+    """Directed graph of a routing regime: row lengths from degree_sequence;
+    a fraction `locality` of each row's columns lies within +-window of the
+    row (banded, as road and web graphs), the rest uniform over the columns,
+    or drawn proportional to the row lengths when `popular` (social-style
+    hubs among the columns).  Duplicates are dropped, so the realised degree
+    features are measured, not assumed.  GCN-normalised fp32 values."""
+    rng = np.random.default_rng(seed)
+    K = M
+    deg = degree_sequence(rng, M, avg_deg, cv, max_deg or min(K, 50_000))
+    rows = np.repeat(np.arange(M, dtype=np.int64), deg)
+    total = rows.size
+    near = rng.random(total) < locality
+    cols = np.empty(total, dtype=np.int64)
+    n_near = int(near.sum())
+    cols[near] = np.clip(rows[near] + rng.integers(-window, window + 1, size=n_near), 0, K - 1)
+    far = ~near
+    if popular:
+        cols[far] = _weighted_endpoints(rng, deg.astype(np.float64), total - n_near)
+    else:
+        cols[far] = rng.integers(0, K, size=total - n_near)
+    rowptr, colind = _csr_from_keys(rows * K + cols, M, K)
+    del rows, cols
+    return Graph(rowptr, colind, gcn_norm_values(rowptr, colind), M, K,
+                 name or f"regime_{M}_{avg_deg}_{cv}")
+
+
+# Calibration suite of the router on gfx950: one or more graphs per region of
+# the seven-rule tree (router/router_dispatch.cpp:1036-1094) that the five
+# benchmark configurations leave empty.  Keys name the rule and branch the
+# graph is built to land in; the realised (d, cv, M) decide.
+REGIMES = {
+    "R1_extreme": lambda: chung_lu(200_000, 8.0, 2.0, 20_000, seed=11),
+    "R2_ultralow_road": lambda: regime_graph(1_000_000, 3.0, 0.3, 0.95, 64, seed=12, name="R2_ultralow_road"),
+    "R2_community_lowd": lambda: regime_graph(200_000, 6.0, 0.4, 0.8, 512, seed=13, name="R2_community_lowd"),
+    "R2_uniform": lambda: er(500_000, 16.0, seed=14),
+    "R3_medium": lambda: regime_graph(100_000, 12.0, 4.0, seed=15, name="R3_medium"),
+    "R3_medium_pop": lambda: regime_graph(150_000, 20.0, 3.5, popular=True, seed=16, name="R3_medium_pop"),
+    "R3_large": lambda: regime_graph(500_000, 12.0, 4.0, seed=17, name="R3_large"),
+    "R4_dense": lambda: regime_graph(50_000, 80.0, 1.0, popular=True, seed=18, name="R4_dense"),
+    "R5_small_dense": lambda: regime_graph(15_000, 30.0, 0.9, seed=19, name="R5_small_dense"),
+    "R5_small_skew": lambda: regime_graph(8_000, 32.0, 1.4, 0.3, 256, popular=True, seed=20,
+                                          name="R5_small_skew"),
+    "R6_heavy": lambda: regime_graph(200_000, 30.0, 2.2, popular=True, seed=21, name="R6_heavy"),
+    "R7_web": lambda: regime_graph(300_000, 6.0, 1.3, 0.7, 256, seed=22, name="R7_web"),
+    "R8_mid": lambda: regime_graph(300_000, 12.0, 1.2, 0.3, 1024, seed=23, name="R8_mid"),
+    "R8_lowd": lambda: regime_graph(500_000, 4.0, 1.0, seed=24, name="R8_lowd"),
+    "R8_small": lambda: regime_graph(20_000, 8.0, 1.0, seed=25, name="R8_small"),
+    "R2_uniform_banded": lambda: regime_graph(300_000, 10.0, 0.3, 0.9, 256, seed=26, name="R2_uniform_banded"),
+    "R3_large_local": lambda: regime_graph(400_000, 10.0, 4.2, 0.5, 512, seed=27, name="R3_large_local"),
+    "R4_dense_wide": lambda: regime_graph(100_000, 60.0, 0.8, seed=28, name="R4_dense_wide"),
+    "R6_heavy_local": lambda: regime_graph(300_000, 28.0, 2.5, 0.5, 512, popular=True, seed=29,
+                                           name="R6_heavy_local"),
+    "R7_web_popular": lambda: regime_graph(500_000, 8.0, 1.2, 0.8, 128, popular=True, seed=30,
+                                           name="R7_web_popular"),
+    "R8_mid_uniform": lambda: regime_graph(200_000, 20.0, 1.0, seed=31, name="R8_mid_uniform"),
+    "R8_lowd_banded": lambda: regime_graph(400_000, 4.5, 0.9, 0.8, 64, seed=32, name="R8_lowd_banded"),
+}
+
+
 CONFIGS = {
     "C1": lambda: er(10_000, 8.0, seed=1),
     "C2": lambda: chung_lu(1_000_000, 16.0, 2.1, 50_000, seed=2),

@@ -160,3 +160,61 @@ def test_chunked_weight_grad_on_device():
         ref = g.double().t() @ x.double()
         scale = g.double().abs().t() @ x.double().abs()
         assert float(((got - ref).abs() / scale).max()) < 1e-5
+
+
+def test_gcn_full_size_c5_step():
+    """One full-size config C5 training step (1e6-row power-law GCN operator,
+    128 -> 256 -> 47) through the router backend against the csr_direct
+    backend (one fp32 fma chain per element, the arithmetic
+    oracle.spmm_seq_f32 pins).  Logits: elementwise, within the propagated
+    bound of 1e-5 |A||B| per SpMM plus the GEMM rounding of the perturbed
+    hidden layer (256 * 2^-24 |H||W2|, twice).  Weight gradients (reductions
+    over all 1e6 rows): max |difference| <= 1e-5 max |gradient|."""
+    S.use_device_sort("cuda")
+    try:
+        g = S.CONFIGS["C5"]()
+    finally:
+        S.use_device_sort(None)
+    M = g.M
+    op = sp.csr_matrix((g.vals, g.colind, g.rowptr), shape=(M, M))
+    torch.manual_seed(0)
+    X = torch.randn(M, 128, device="cuda")
+    y = torch.randint(0, 47, (M,), device="cuda")
+    res = {}
+    for backend in ("router", "csr_direct"):
+        print(f"[c5 gcn step] {backend}", flush=True)
+        torch.manual_seed(1)
+        model = gnn.GCN(128, 256, 47).cuda()
+        graph = gnn.GraphBackend(op, "cuda")
+        out = model(X, graph, backend)
+        gnn.cross_entropy(out, y).backward()
+        labels = {k: lab for k, (lab, _) in graph.exec_cache.items()}
+        res[backend] = (out.detach(), [p.grad.detach().clone() for p in model.parameters()], labels)
+        del graph, model
+        torch.cuda.empty_cache()
+    # the router routes all four SpMMs (forward and backward, N = 256 and 47)
+    assert len(res["router"][2]) == 4 and set(res["router"][2].values()) == {"ZERO_OVERHEAD_CSR"}
+    out_r, grads_r, _ = res["router"]
+    out_c, grads_c, _ = res["csr_direct"]
+    rp, ci, vl = g.torch("cuda")
+    va = vl.abs()
+
+    def spmm(vals, B):
+        return ra_spmm.spmm_csr_direct(rp, ci, vals, B.contiguous())
+
+    torch.manual_seed(1)
+    ref = gnn.GCN(128, 256, 47).cuda()
+    W1, W2 = ref.lin1.weight.detach(), ref.lin2.weight.detach()
+    with torch.no_grad():
+        XW1 = X @ W1.t()
+        H = F.relu(spmm(vl, XW1))
+        s1 = spmm(va, XW1.abs())
+        HW2a = H.abs() @ W2.abs().t()
+        bound = (1e-5 * spmm(va, (H @ W2.t()).abs()) + spmm(va, (1e-5 * s1) @ W2.abs().t())
+                 + 2.0 * 256 * 2.0 ** -24 * spmm(va, HW2a))
+        err = (out_r - out_c).abs()
+        bad = err > bound + 1e-30
+        assert not bool(bad.any()), (int(bad.sum()), float(err.max()))
+    for name, gr, gc in zip(("lin1", "lin2"), grads_r, grads_c):
+        diff = float((gr - gc).abs().max())
+        assert diff <= 1e-5 * float(gc.abs().max()), (name, diff, float(gc.abs().max()))

@@ -162,10 +162,11 @@ def test_c3_full_size_properties(oracle, N):
 
 def test_c4_full_size_properties(oracle):
     """config C4 (log-normal degrees to 20k, fp16 values) at full size through
-    the routed COMMUNITY_TC and TC_DIRECT with the automatic 8 column
-    partitions: a row sample (including the 20 longest rows) against the
-    oracle at N=512 on the FP16 route (1e-5) and the FP32 route (bit-exact),
-    and the all-ones row sums on every row."""
+    the routed COMMUNITY_TC, TC_DIRECT and SEGMENT_HYBRID with the automatic 8
+    column partitions: a row sample (including the 20 longest rows) against
+    the oracle at N=512 on the FP16 route (1e-5) and the FP32 route
+    (bit-exact), the all-ones row sums on every row, and a second call
+    bit-identical to the first (the split windows' merge is deterministic)."""
     g = S.CONFIGS["C4"]()
     gd = g.torch("cuda")
     N = 512
@@ -181,12 +182,13 @@ def test_c4_full_size_properties(oracle):
     scale = oracle.spmm_f64(sub_rp, sub_ci, np.abs(sub_vl), np.abs(B))
     exact = np.add.reduceat(np.append(g.vals.astype(np.float64), 0), g.rowptr[:-1])
     exact[deg == 0] = 0
-    for kind in (1, 0):
+    for kind in (1, 0, 2):
         print(f"[c4 full] kind={kind}", flush=True)
         plan = MAKE[kind](gd[0], gd[1], gd[2], g.M, g.K, N)
         assert plan.col_parts == 8 and plan.rows_per_window == 8
         C = run(kind, plan, Bd, "f16", gd)
         assert_close_scaled(C.cpu().numpy()[rows], ref, scale, 1e-5, f"C4 kind {kind}")
+        assert torch.equal(C, run(kind, plan, Bd, "f16", gd)), f"C4 kind {kind}: second call differs"
         del C
         # FP32 route over the 8 column ranges: one fma chain per element in
         # ascending column order (values are fp16-representable: stored exactly).
@@ -194,6 +196,41 @@ def test_c4_full_size_properties(oracle):
         np.testing.assert_array_equal(C32, oracle.spmm_seq_f32(sub_rp, sub_ci, sub_vl, B), err_msg=f"C4 fp32 {kind}")
         ones = torch.ones(g.K, 16, device="cuda")
         rs = run(kind, plan, ones, "f16", gd)[:, 0].double().cpu().numpy()
+        assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
+        del plan
+        torch.cuda.empty_cache()
+
+
+def test_c4_full_size_bf16(oracle):
+    """config C4 at full size with bf16-valued plans of every kind (bf16 B,
+    N=512, 8 column partitions): a row sample with the 20 longest rows against
+    the fp64 product of the bf16-quantised inputs (1e-5), the all-ones row sums
+    against the bf16-rounded values (1e-5), and a repeated call bit-identical."""
+    g = S.CONFIGS["C4"]()
+    gd = g.torch("cuda")
+    N = 512
+    B = np.random.default_rng(5).standard_normal((g.K, N)).astype(np.float32)
+    Bd = torch.from_numpy(oracle.quantize_bf16(B).astype(np.float32)).cuda().to(torch.bfloat16)
+    deg = np.diff(g.rowptr)
+    rows = np.unique(np.concatenate([np.arange(0, g.M, 2003), np.argsort(deg)[-20:]]))
+    sub_rp = np.concatenate([[0], np.cumsum(deg[rows])]).astype(np.int32)
+    sub_ci = np.concatenate([g.colind[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    sub_vl = np.concatenate([g.vals[g.rowptr[r]:g.rowptr[r + 1]] for r in rows])
+    ref = oracle.spmm_tile_f64(sub_rp, sub_ci, sub_vl, B, "bf16")
+    scale = oracle.spmm_f64(sub_rp, sub_ci, np.abs(oracle.quantize_bf16(sub_vl)), np.abs(oracle.quantize_bf16(B)))
+    qv = oracle.quantize_bf16(g.vals).astype(np.float64)
+    exact = np.add.reduceat(np.append(qv, 0), g.rowptr[:-1])
+    exact[deg == 0] = 0
+    for kind in (1, 0, 2):
+        print(f"[c4 full bf16] kind={kind}", flush=True)
+        plan = MAKE[kind](gd[0], gd[1], gd[2], g.M, g.K, N, "bf16")
+        assert plan.col_parts == 8
+        C = run(kind, plan, Bd, "bf16", gd)
+        assert_close_scaled(C.cpu().numpy()[rows], ref, scale, 1e-5, f"C4 bf16 kind {kind}")
+        assert torch.equal(C, run(kind, plan, Bd, "bf16", gd)), f"C4 bf16 kind {kind}: second call differs"
+        del C
+        ones = torch.ones(g.K, 16, device="cuda", dtype=torch.bfloat16)
+        rs = run(kind, plan, ones, "bf16", gd)[:, 0].double().cpu().numpy()
         assert np.all(np.abs(rs - exact) <= 1e-5 * np.maximum(1, np.abs(exact)))
         del plan
         torch.cuda.empty_cache()
