@@ -644,6 +644,46 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
     return out
 
 
+def route_probe(cfgs=("C1", "C2"), N=128, reps=200, table="mi355x"):
+    """Cold routing cost, broken down: make_router_plan on device tensors (GPU
+    feature pass + rule tree + plan dict) and on host tensors, the feature
+    pass alone, and the rule tree + dict alone (route_features).  Wall-clock
+    means over `reps` calls, each call synchronised first as a cold caller is."""
+    import torch
+    import ra_spmm
+    from ra_spmm import synthetic as S
+    S.use_device_sort("cuda")
+    out = {}
+    for cfg in cfgs:
+        g = S.CONFIGS[cfg]()
+        rp, ci, vl = g.torch("cuda")
+        hrp, hci, hvl = rp.cpu(), ci.cpu(), vl.cpu()
+        f = ra_spmm.compute_features(rp, g.M, g.K, N)
+
+        def mean_us(fn):
+            fn()
+            ts = []
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t)
+            ts.sort()
+            return {"mean_us": round(1e6 * sum(ts) / len(ts), 2), "median_us": round(1e6 * ts[len(ts) // 2], 2)}
+        rec = {
+            "make_router_plan_device": mean_us(lambda: ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N, "MAIN", table)),
+            "make_router_plan_host": mean_us(lambda: ra_spmm.make_router_plan(hrp, hci, hvl, g.M, g.K, N, "MAIN", table)),
+            "features_device": mean_us(lambda: ra_spmm.compute_features(rp, g.M, g.K, N)),
+            "features_host": mean_us(lambda: ra_spmm.compute_features(hrp, g.M, g.K, N)),
+            "route_and_dict": mean_us(lambda: ra_spmm.route_features(g.M, g.K, N, f["nnz"], f["sum_deg_sq"],
+                                                                     f["max_deg"], f["empty_rows"], "MAIN", table)),
+        }
+        out[f"{cfg}_N{N}"] = rec
+        log(f"[route] {cfg} M={g.M}: {json.dumps(rec)}")
+        del rp, ci, vl
+    return out
+
+
 def sweep(configs, Ns, steps, out_path):
     """Every deployed path on each config (calibration of the MI355X table)."""
     import torch
@@ -749,6 +789,8 @@ def main(argv=None):
     ap.add_argument("--sweep-out", default=None, help="write the sweep rows here as JSON")
     ap.add_argument("--details", default=None, help="write the full result dict here")
     ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
+    ap.add_argument("--route-probe", action="store_true",
+                    help="cold routing cost (make_router_plan) broken down on C1 and C2")
     ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
     ap.add_argument("--gcn", action="store_true", help="config 5 GCN training step (details on stderr)")
     ap.add_argument("--gcn-backends", default="router,router_cold,rocsparse,cusparse,zero_overhead,csr_direct",
@@ -774,6 +816,9 @@ def main(argv=None):
         return 0
     if args.gather_sweep:
         gather_sweep(args.details)
+        return 0
+    if args.route_probe:
+        print(json.dumps({"route_probe": route_probe(table=args.table)}), flush=True)
         return 0
     if args.sweep:
         names = []

@@ -21,6 +21,7 @@
 // the reference per-lane accumulation (csr/csr_direct.cu:201-228).
 #include <algorithm>
 #include <cstdlib>
+#include <chrono>
 #include <mutex>
 
 #include "ra_internal.hpp"
@@ -388,18 +389,36 @@ __device__ __forceinline__ int wave_max_i(int v) {
     return v;
 }
 
-// Per-block partials: [block][0] = sum d^2, [1] = max d, [2] = empty rows.
-__global__ __launch_bounds__(kBlock) void degree_moments_partial(
-    const int32_t* __restrict__ rowptr, int M, long long* __restrict__ part) {
-    __shared__ long long s_sq[kWavesPerBlock], s_em[kWavesPerBlock];
-    __shared__ int s_mx[kWavesPerBlock];
+// Block sums of (d^2, empty rows) and the block max of d over the rows
+// blockIdx.x * BS + threadIdx.x + k * gridDim.x * BS; valid in thread 0.
+template <int BS>
+__device__ __forceinline__ void block_moments(const int32_t* __restrict__ rowptr, int M,
+                                              long long& sq_out, int& mx_out, long long& em_out) {
+    constexpr int W = BS / kWave;
+    __shared__ long long s_sq[W], s_em[W];
+    __shared__ int s_mx[W];
     long long sq = 0, em = 0;
     int mx = 0;
-    for (int r = blockIdx.x * kBlock + threadIdx.x; r < M; r += gridDim.x * kBlock) {
-        const long long d = (long long)rowptr[r + 1] - rowptr[r];
-        sq += d * d;
-        em += (d == 0);
-        mx = max(mx, (int)d);
+    // Eight rows per thread per step, their loads issued together (a strided
+    // loop with one row per step waits one memory latency per row).
+    constexpr int kU = 8;
+    const int stride = gridDim.x * BS;
+    for (int r0 = blockIdx.x * BS + threadIdx.x; r0 < M; r0 += kU * stride) {
+        int lo[kU], hi[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int r = r0 + u * stride;
+            lo[u] = r < M ? rowptr[r] : 0;
+            hi[u] = r < M ? rowptr[r + 1] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            if (r0 + u * stride >= M) break;
+            const long long d = (long long)hi[u] - lo[u];
+            sq += d * d;
+            em += (d == 0);
+            mx = max(mx, (int)d);
+        }
     }
     sq = wave_sum_ll(sq);
     em = wave_sum_ll(em);
@@ -412,23 +431,57 @@ __global__ __launch_bounds__(kBlock) void degree_moments_partial(
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        long long a = 0, e = 0;
-        int m = 0;
-        for (int w = 0; w < kWavesPerBlock; ++w) {
-            a += s_sq[w];
-            e += s_em[w];
-            m = max(m, s_mx[w]);
+        sq = em = 0;
+        mx = 0;
+        for (int w = 0; w < W; ++w) {
+            sq += s_sq[w];
+            em += s_em[w];
+            mx = max(mx, s_mx[w]);
         }
-        part[blockIdx.x * 3 + 0] = a;
-        part[blockIdx.x * 3 + 1] = m;
-        part[blockIdx.x * 3 + 2] = e;
+        sq_out = sq;
+        mx_out = mx;
+        em_out = em;
     }
 }
 
-// Single block: out = {nnz, sum d^2, max d, empty rows}.
+// out (mapped pinned host memory) = {nnz, sum d^2, max d, empty rows, seq}:
+// the four values, a system-scope fence, then the call's sequence number, so a
+// host that reads seq back sees the values of this call.
+__device__ __forceinline__ void publish_moments(long long* out, long long nnz, long long sq, int mx,
+                                                long long em, long long seq) {
+    out[0] = nnz;
+    out[1] = sq;
+    out[2] = mx;
+    out[3] = em;
+    __threadfence_system();
+    __hip_atomic_store(&out[4], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// A small matrix in one block of 1024 lanes, which writes the result itself.
+__global__ __launch_bounds__(1024) void degree_moments_one(const int32_t* __restrict__ rowptr, int M,
+                                                           long long* __restrict__ out, long long seq) {
+    long long sq = 0, em = 0;
+    int mx = 0;
+    block_moments<1024>(rowptr, M, sq, mx, em);
+    if (threadIdx.x == 0) publish_moments(out, (long long)rowptr[M] - rowptr[0], sq, mx, em, seq);
+}
+
+// Per-block partials: [block][0] = sum d^2, [1] = max d, [2] = empty rows.
+__global__ __launch_bounds__(kBlock) void degree_moments_partial(const int32_t* __restrict__ rowptr, int M,
+                                                                 long long* __restrict__ part) {
+    long long sq = 0, em = 0;
+    int mx = 0;
+    block_moments<kBlock>(rowptr, M, sq, mx, em);
+    if (threadIdx.x != 0) return;
+    part[blockIdx.x * 3 + 0] = sq;
+    part[blockIdx.x * 3 + 1] = mx;
+    part[blockIdx.x * 3 + 2] = em;
+}
+
+// Single block: out = {nnz, sum d^2, max d, empty rows} from the partials.
 __global__ __launch_bounds__(kBlock) void degree_moments_final(
     const long long* __restrict__ part, int nparts, const int32_t* __restrict__ rowptr, int M,
-    long long* __restrict__ out) {
+    long long* __restrict__ out, long long seq) {
     __shared__ long long s_sq[kWavesPerBlock], s_em[kWavesPerBlock];
     __shared__ int s_mx[kWavesPerBlock];
     long long sq = 0, em = 0;
@@ -456,18 +509,20 @@ __global__ __launch_bounds__(kBlock) void degree_moments_final(
             e += s_em[w];
             m = max(m, s_mx[w]);
         }
-        out[0] = (long long)rowptr[M] - rowptr[0];
-        out[1] = a;
-        out[2] = m;
-        out[3] = e;
+        publish_moments(out, (long long)rowptr[M] - rowptr[0], a, m, e, seq);
     }
 }
+
+// Rows up to which one block reduces the whole rowptr (one launch; a second,
+// dependent launch costs ~7 us of queue latency on MI355X).
+constexpr int kMomentOneBlockRows = 1 << 16;
 
 // Per-device reduction buffers, allocated once and kept for the process.
 struct MomentBuffers {
     long long* part = nullptr;
-    long long* result = nullptr;
-    long long* host = nullptr;  // pinned
+    long long* host = nullptr;       // pinned, mapped: the kernels write the result here
+    long long* host_dev = nullptr;   // its device address
+    long long seq = 0;               // sequence number of the last call
 };
 std::mutex g_moment_mutex;
 MomentBuffers g_moment[64];
@@ -768,21 +823,46 @@ ra_status ra_features_device(const int32_t* d_rowptr, int32_t M, int32_t K, int3
     RA_HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= 64) return ra::fail(RA_ERR_UNSUPPORTED, "features: device id >= 64");
     MomentBuffers* mb = &g_moment[dev];
-    {
-        std::lock_guard<std::mutex> lock(g_moment_mutex);
-        if (!mb->part) {
-            RA_HIP_TRY(hipMalloc(&mb->part, sizeof(long long) * 3 * kMomentBlocks));
-            RA_HIP_TRY(hipMalloc(&mb->result, sizeof(long long) * 4));
-            RA_HIP_TRY(hipHostMalloc(&mb->host, sizeof(long long) * 4, hipHostMallocDefault));
-        }
+    // One feature pass at a time per process: the buffers are per device and
+    // the wait below reads them back (a pass takes ~15 us).
+    std::lock_guard<std::mutex> lock(g_moment_mutex);
+    if (!mb->part) {
+        RA_HIP_TRY(hipMalloc(&mb->part, sizeof(long long) * 3 * kMomentBlocks));
+        RA_HIP_TRY(hipHostMalloc(&mb->host, sizeof(long long) * 5,
+                                 hipHostMallocMapped | hipHostMallocCoherent));
+        mb->host[4] = 0;
+        RA_HIP_TRY(hipHostGetDevicePointer(reinterpret_cast<void**>(&mb->host_dev), mb->host, 0));
     }
-    const int blocks = std::max(1, std::min(kMomentBlocks, (M + kBlock * 4 - 1) / (kBlock * 4)));
-    degree_moments_partial<<<blocks, kBlock, 0, st>>>(d_rowptr, M, mb->part);
-    RA_LAUNCH_CHECK("degree_moments_partial");
-    degree_moments_final<<<1, kBlock, 0, st>>>(mb->part, blocks, d_rowptr, M, mb->result);
-    RA_LAUNCH_CHECK("degree_moments_final");
-    RA_HIP_TRY(hipMemcpyAsync(mb->host, mb->result, sizeof(long long) * 4, hipMemcpyDeviceToHost, st));
-    RA_HIP_TRY(hipStreamSynchronize(st));
+    // The result goes straight to mapped pinned host memory (no copy).
+    const long long seq = ++mb->seq;
+    if (M <= kMomentOneBlockRows) {
+        degree_moments_one<<<1, 1024, 0, st>>>(d_rowptr, M, mb->host_dev, seq);
+        RA_LAUNCH_CHECK("degree_moments_one");
+    } else {
+        const int blocks = std::max(2, std::min(kMomentBlocks, (M + kBlock * 4 - 1) / (kBlock * 4)));
+        degree_moments_partial<<<blocks, kBlock, 0, st>>>(d_rowptr, M, mb->part);
+        RA_LAUNCH_CHECK("degree_moments_partial");
+        degree_moments_final<<<1, kBlock, 0, st>>>(mb->part, blocks, d_rowptr, M, mb->host_dev, seq);
+        RA_LAUNCH_CHECK("degree_moments_final");
+    }
+    // Wait by polling the sequence number the last kernel publishes (a
+    // stream synchronisation adds ~5 us to a ~15 us call).  After ~200 us
+    // (earlier work queued on the stream, or a failed kernel) fall back to
+    // the synchronisation, which returns any launch or execution error.
+    long long* flag = mb->host + 4;
+    bool seen = false;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int spin = 0; !seen; ++spin) {
+        seen = __atomic_load_n(flag, __ATOMIC_ACQUIRE) == seq;
+        if (!seen && (spin & 1023) == 1023 &&
+            std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(200))
+            break;
+    }
+    if (!seen) {
+        RA_HIP_TRY(hipStreamSynchronize(st));
+        if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) != seq)
+            return ra::fail(RA_ERR_INTERNAL, "features: the reduction did not publish its result");
+    }
     return ra_features_from_moments(M, K, N, mb->host[0], mb->host[1],
                                     static_cast<int32_t>(mb->host[2]), mb->host[3], out);
 }

@@ -255,10 +255,35 @@ pybind11::dict features_to_dict(const ra_features& f) {
     return d;
 }
 
+// Python strings of the plan dict, made once: a dict of 15 paths built from
+// C strings costs ~5 us per routing call, most of it in string creation.
+// Deliberately leaked, so no destructor runs after the interpreter is gone.
+struct DictStrings {
+    pybind11::str path[RA_PATH_COUNT];
+    pybind11::str reject[RA_REJECT_UNKNOWN + 1];
+    pybind11::str detail[RA_PATH_COUNT][3];  // N < 16, not built, not in portfolio
+    pybind11::str empty;
+    DictStrings() : empty("") {
+        for (int p = 0; p < RA_PATH_COUNT; ++p) {
+            const std::string name = ra_path_name(p);
+            path[p] = pybind11::str(name);
+            detail[p][0] = pybind11::str("N < 16");
+            detail[p][1] = pybind11::str("not built for MI355X");
+            detail[p][2] = pybind11::str(name + " not in selected portfolio");
+        }
+        for (int c = 0; c <= RA_REJECT_UNKNOWN; ++c) reject[c] = pybind11::str(ra_reject_name(c));
+    }
+};
+const DictStrings& dict_strings() {
+    static const DictStrings* s = new DictStrings();
+    return *s;
+}
+
 // bindings/ra_bindings.cpp:634-718 (plan_to_dict) + :1717-1753 (make_router_plan_fn)
 pybind11::dict route_to_dict(const ra_features& f, const ra_route& r, float ms) {
+    const DictStrings& S = dict_strings();
     pybind11::dict d;
-    d["chosen_path"] = std::string(ra_path_name(r.chosen_path));
+    d["chosen_path"] = S.path[r.chosen_path];
     d["use_tf32"] = static_cast<bool>(r.use_tf32);
     d["chosen_path_int"] = r.chosen_path;
     d["decision_reason"] = std::string(r.decision_reason);
@@ -270,19 +295,20 @@ pybind11::dict route_to_dict(const ra_features& f, const ra_route& r, float ms) 
     d["est_plan_s"] = r.est_plan_s;
     d["tile_ok"] = static_cast<bool>(r.tile_ok);
     d["path_count"] = static_cast<int>(RA_PATH_COUNT);
-    pybind11::list names, feas;
+    pybind11::list names(static_cast<size_t>(RA_PATH_COUNT)), feas(static_cast<size_t>(RA_PATH_COUNT));
     pybind11::dict by_path, codes, details;
     for (int p = 0; p < RA_PATH_COUNT; ++p) {
-        const std::string name = ra_path_name(p);
-        names.append(name);
-        feas.append(static_cast<bool>(r.feasible[p]));
-        by_path[name.c_str()] = static_cast<bool>(r.feasible[p]);
-        codes[name.c_str()] = std::string(ra_reject_name(r.rejection_code[p]));
-        std::string detail;
-        if (r.rejection_code[p] == RA_REJECT_MARGIN_TOO_SMALL) detail = "N < 16";
-        else if (r.rejection_code[p] == RA_REJECT_NOT_FEASIBLE) detail = "not built for MI355X";
-        else if (r.rejection_code[p] == RA_REJECT_NOT_IN_PORTFOLIO) detail = name + " not in selected portfolio";
-        details[name.c_str()] = detail;
+        const pybind11::str& name = S.path[p];
+        const bool ok = r.feasible[p] != 0;
+        names[p] = name;
+        feas[p] = pybind11::bool_(ok);
+        by_path[name] = pybind11::bool_(ok);
+        const int code = r.rejection_code[p];
+        codes[name] = S.reject[(code < 0 || code > RA_REJECT_UNKNOWN) ? RA_REJECT_UNKNOWN : code];
+        details[name] = code == RA_REJECT_MARGIN_TOO_SMALL  ? S.detail[p][0]
+                        : code == RA_REJECT_NOT_FEASIBLE     ? S.detail[p][1]
+                        : code == RA_REJECT_NOT_IN_PORTFOLIO ? S.detail[p][2]
+                                                             : S.empty;
     }
     d["path_names"] = names;
     d["feasible"] = feas;
