@@ -684,6 +684,63 @@ def route_probe(cfgs=("C1", "C2"), N=128, reps=200, table="mi355x"):
     return out
 
 
+def bf16x3_probe(cfgs=("C2", "C5"), Ns=(128, 256), steps=20, kind="COMMUNITY_TC"):
+    """A stated-tolerance route for fp32 data on the MFMA kernels, measured
+    before it is built: A = Ahi + Alo and B = Bhi + Blo with bf16 halves, and
+    C ~ Ahi Bhi + Ahi Blo + Alo Bhi (the Alo Blo term, ~2^-16 relative, is
+    dropped).  Here it is composed from three bf16 calls of the tile kernel
+    plus two adds (an upper bound on a fused kernel's time). The fused
+    kernel's gathers, a hi and a lo half of every B row, are the bytes of one
+    16-bit call at 2N, which is timed as its estimate.  Error: elementwise
+    |C - C64| / (|A||B|) against a float64 torch.sparse product on the GPU."""
+    import torch
+    import ra_spmm
+    from ra_spmm import synthetic as S
+    S.use_device_sort("cuda")
+    make = {"COMMUNITY_TC": ra_spmm.make_community_tc_plan, "TC_DIRECT": ra_spmm.make_tc_direct_plan,
+            "SEGMENT_HYBRID": ra_spmm.make_segment_hybrid_plan}[kind]
+    out = {}
+    for cfg in cfgs:
+        g = S.CONFIGS[cfg]()
+        rp, ci, vl = g.torch("cuda")
+        vhi = vl.to(torch.bfloat16).float()
+        vlo = (vl - vhi).to(torch.bfloat16).float()
+        p_hi = make(rp, ci, vl, g.M, g.K, max(Ns), "bf16")
+        p_lo = make(rp, ci, vlo, g.M, g.K, max(Ns), "bf16")
+        A64 = torch.sparse_csr_tensor(rp.long(), ci.long(), vl.double(), size=(g.M, g.K))
+        Aabs = torch.sparse_csr_tensor(rp.long(), ci.long(), vl.double().abs(), size=(g.M, g.K))
+        zo = ra_spmm.make_zero_overhead_plan(rp.cpu(), g.M, g.K)
+        for N in Ns:
+            B = torch.randn(g.K, N, device="cuda", generator=torch.Generator(device="cuda").manual_seed(N))
+            Bhi = B.to(torch.bfloat16)
+            Blo = (B - Bhi.float()).to(torch.bfloat16)
+            run = ra_spmm.run_tile_plan_route
+
+            def three():
+                return run(p_hi, Bhi, "bf16") + run(p_hi, Blo, "bf16") + run(p_lo, Bhi, "bf16")
+            B2 = torch.cat([Bhi, Blo], dim=1).contiguous()
+            t3, _ = timed_steps(three, steps, 3)
+            t1, _ = timed_steps(lambda: run(p_hi, Bhi, "bf16"), steps, 3)
+            t2n, _ = timed_steps(lambda: run(p_hi, B2, "bf16"), steps, 3)
+            tzo, _ = timed_steps(lambda: ra_spmm.run_zero_overhead_plan(zo, rp, ci, vl, B), steps, 3)
+            C = three().double()
+            C64 = torch.sparse.mm(A64, B.double())
+            scale = torch.sparse.mm(Aabs, B.double().abs())
+            err3 = float(((C - C64).abs() / (scale + 1e-300)).max())
+            C1 = run(p_hi, Bhi, "bf16").double()
+            err1 = float(((C1 - C64).abs() / (scale + 1e-300)).max())
+            rec = {"kind": kind, "bf16x3_three_calls_ms": round(t3, 4), "bf16x3_fused_estimate_ms": round(t2n, 4),
+                   "bf16_one_call_ms": round(t1, 4), "zero_overhead_fp32_ms": round(tzo, 4),
+                   "bf16x3_max_rel_err": err3, "bf16_max_rel_err": err1}
+            out[f"{cfg}_N{N}"] = rec
+            log(f"[bf16x3] {cfg} N={N}: {json.dumps(rec)}")
+            del B, Bhi, Blo, B2, C, C64, scale, C1
+            torch.cuda.empty_cache()
+        del p_hi, p_lo, A64, Aabs, zo, rp, ci, vl, vhi, vlo
+        torch.cuda.empty_cache()
+    return out
+
+
 def sweep(configs, Ns, steps, out_path):
     """Every deployed path on each config (calibration of the MI355X table)."""
     import torch
@@ -789,6 +846,8 @@ def main(argv=None):
     ap.add_argument("--sweep-out", default=None, help="write the sweep rows here as JSON")
     ap.add_argument("--details", default=None, help="write the full result dict here")
     ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
+    ap.add_argument("--bf16x3-probe", action="store_true",
+                    help="time and error of a bf16x3 split route for fp32 data on C2 and C5")
     ap.add_argument("--route-probe", action="store_true",
                     help="cold routing cost (make_router_plan) broken down on C1 and C2")
     ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
@@ -816,6 +875,9 @@ def main(argv=None):
         return 0
     if args.gather_sweep:
         gather_sweep(args.details)
+        return 0
+    if args.bf16x3_probe:
+        print(json.dumps({"bf16x3_probe": bf16x3_probe()}), flush=True)
         return 0
     if args.route_probe:
         print(json.dumps({"route_probe": route_probe(table=args.table)}), flush=True)
