@@ -741,6 +741,57 @@ def bf16x3_probe(cfgs=("C2", "C5"), Ns=(128, 256), steps=20, kind="COMMUNITY_TC"
     return out
 
 
+def order_study(cfg="C4", heights=(8, 16, 32), g=None):
+    """Host-side study (no GPU): B rows gathered by a tile plan (= vectors =
+    distinct columns per window, summed over windows) under candidate row
+    orders and window heights.  nnz / vectors is the nonzeros each gathered
+    B row serves; the MFMA tile kernels are bound by the gathers."""
+    import numpy as np
+    from ra_spmm import synthetic as S
+    if g is None:
+        g = S.CONFIGS[cfg]()
+    rp = g.rowptr.astype(np.int64)
+    ci = g.colind.astype(np.int64)
+    M = g.M
+    deg = np.diff(rp)
+    rows_of = np.repeat(np.arange(M), deg)
+    ident = np.arange(M)
+    lead = np.where(deg > 0, ci[np.minimum(rp[:-1], max(int(rp[-1]) - 1, 0))], np.iinfo(np.int64).max)
+    indeg = np.bincount(ci, minlength=g.K)
+    by_pop = np.lexsort((-indeg[ci], rows_of))  # within each row, most popular column first
+    top = np.where(deg > 0, ci[by_pop[np.minimum(rp[:-1], max(int(rp[-1]) - 1, 0))]], -1)
+    rng = np.random.default_rng(0)
+    a, b = int(rng.integers(1, 2 ** 31 - 1)), int(rng.integers(0, 2 ** 31 - 1))
+    mh = np.full(M, np.iinfo(np.int64).max)
+    np.minimum.at(mh, rows_of, (a * ci + b) % 2147483647)
+    # The diagnostic reorder of router/router_features.cpp:271-285: 16 buckets
+    # of the mean column, then column span ascending, then length descending.
+    csum = np.zeros(M)
+    np.add.at(csum, rows_of, ci.astype(np.float64))
+    bucket = np.where(deg > 0, (csum / np.maximum(deg, 1) * 16.0 / g.K).astype(np.int64), 0)
+    lo = np.where(deg > 0, ci[np.minimum(rp[:-1], max(int(rp[-1]) - 1, 0))], 0)
+    hi = np.where(deg > 0, ci[np.maximum(rp[1:] - 1, 0)], 0)
+    span = np.where(deg > 0, hi - lo + 1, g.K)
+    orders = {
+        "identity (TC_DIRECT)": ident,
+        "centroid bucket, span, length (diagnostic reorder)": np.lexsort((ident, -deg, span, bucket)),
+        "leading column (COMMUNITY_TC)": np.lexsort((ident, lead)),
+        "most popular column": np.lexsort((ident, top)),
+        "minhash of the column set": np.lexsort((ident, mh)),
+        "row length, descending": np.lexsort((ident, -deg)),
+        "row length desc., then most popular column": np.lexsort((top, -deg)),
+    }
+    out = {"config": cfg, "nnz": g.nnz, "rows": {}}
+    for name, order in orders.items():
+        pos = np.empty(M, np.int64)
+        pos[order] = np.arange(M)
+        for H in heights:
+            v = int(np.unique((pos[rows_of] // H) * g.K + ci).size)
+            out["rows"][f"{name} | H={H}"] = {"gathered_rows": v, "nnz_per_gathered_row": round(g.nnz / v, 4)}
+            log(f"[order] {name:45s} H={H:2d} gathered B rows {v:11d}  nnz per row {g.nnz / v:.3f}")
+    return out
+
+
 def sweep(configs, Ns, steps, out_path):
     """Every deployed path on each config (calibration of the MI355X table)."""
     import torch
@@ -846,6 +897,8 @@ def main(argv=None):
     ap.add_argument("--sweep-out", default=None, help="write the sweep rows here as JSON")
     ap.add_argument("--details", default=None, help="write the full result dict here")
     ap.add_argument("--path", default=None, help="force a kernel path instead of the router's pick")
+    ap.add_argument("--order-study", default=None, choices=["C1", "C2", "C3", "C4", "C5"],
+                    help="host-only: B rows a tile plan gathers under candidate row orders and heights")
     ap.add_argument("--bf16x3-probe", action="store_true",
                     help="time and error of a bf16x3 split route for fp32 data on C2 and C5")
     ap.add_argument("--route-probe", action="store_true",
@@ -861,6 +914,9 @@ def main(argv=None):
               f"(the SpMM shards by row blocks, see the sharding notes; run with --gpus 1)",
               file=sys.stderr)
         return 2
+    if args.order_study:  # host only
+        print(json.dumps({"order_study": order_study(args.order_study)}), flush=True)
+        return 0
     import torch
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)

@@ -58,3 +58,18 @@ def test_block_of_carries_the_driver_fields():
     # a tile plan's probe walks its vector columns and is keyed plan_order
     res["gather_ceiling"] = {"plan_order": {"ms": 0.45, "gathers": 10}}
     assert bench.block_of(res)["roofline"]["frac_of_gather_probe"] == round(0.45 / 0.9, 4)
+
+
+def test_order_study_counts_the_plans_vectors():
+    """The study's gathered-row count for the identity and leading-column
+    orders at 8-row windows equals the vector count of the oracle's
+    TC_DIRECT and COMMUNITY_TC formats (a vector = one gathered B row)."""
+    import numpy as np
+    from oracle import oracle as O
+    from ra_spmm import synthetic as S
+    g = S.random_csr(301, 280, 6.0, seed=1, skew=1.1, empty_frac=0.05)
+    study = bench.order_study(heights=(8,), g=g)["rows"]
+    for kind, name in ((0, "identity (TC_DIRECT)"), (1, "leading column (COMMUNITY_TC)")):
+        fmt = O.tile_format(kind, g.rowptr, g.colind, g.vals, g.M)
+        vectors = int(np.count_nonzero(np.any(fmt["blocks"] != 0, axis=1)))
+        assert study[f"{name} | H=8"]["gathered_rows"] == vectors, name
