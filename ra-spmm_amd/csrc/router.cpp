@@ -64,7 +64,9 @@ constexpr RouterTable kReference = {
 // MI355X calibration.  The structure of the tree is unchanged; each knob is
 // set from one measured sweep on gfx950 (bench.py --sweep regimes,C1,...,C5
 // at N = 64, 128, 256, 512: 27 graphs, 108 points, at least one graph in every
-// branch of the tree; router_eval.py scores a table against it):
+// branch of the tree; router_eval.py scores a table against it).  On that
+// sweep this table picks the fastest path on 67 of 108 points (the reference
+// table: 38) at a router/oracle geomean of 0.943 (0.865):
 //  - tile gate: the device tile build runs at 1.0-1.9e-10 s per nnz, plus
 //    ~3e-10 s per nnz to upload a host CSR, so the estimate is 1e-9 s per nnz
 //    with the same 20 s budget;
@@ -74,9 +76,9 @@ constexpr RouterTable kReference = {
 //    (one lane group per hub row is 6.6x slower on config 2);
 //  - rule 2, uniform graphs of d >= 7 at N <= 64 go to CSR_DIRECT (config 3
 //    0.212 vs 0.218 ms for TC_DIRECT);
-//  - rules 3, 5 and 6 pick SEGMENT_HYBRID: the fastest path on 25 of the 32
-//    points of those regions and within 12% on the rest (rule 5's guardrail
-//    pick, the baseline kernel, was 4-6x slower; rule 6's COMMUNITY_TC 1.5x
+//  - rules 3, 5 and 6 pick SEGMENT_HYBRID: the fastest path on 26 of the 32
+//    points of those regions and within 19% on the rest (rule 5's guardrail
+//    pick, the baseline kernel, was 5-6x slower; rule 6's COMMUNITY_TC 1.5x
 //    slower on a graph with local columns; rule 3's split on M gave
 //    COMMUNITY_TC to large graphs, where it was 0-40% slower);
 //  - rule 7 picks TC_DIRECT without forcing the FP32 route (fastest on 5 of

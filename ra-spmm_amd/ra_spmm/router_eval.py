@@ -31,7 +31,7 @@ KERNELS = ("CSR_DIRECT", "ZERO_OVERHEAD_CSR", "TC_DIRECT", "COMMUNITY_TC", "SEGM
            "TC_DIRECT_TF32", "COMMUNITY_TC_TF32", "SEGMENT_HYBRID_TF32")
 GUARDRAIL = "CUSPARSE"
 
-__all__ = ["KERNELS", "points_from_sweep", "evaluate", "format_report", "main"]
+__all__ = ["KERNELS", "points_from_sweep", "rows_from_csv", "evaluate", "format_report", "main"]
 
 
 def _geomean(xs):
@@ -58,6 +58,24 @@ def points_from_sweep(rows, time_key: str = "ms"):
         elif path in KERNELS and r.get("gate_ok", True):
             p["times"][path] = float(r[time_key])
     return dict(pts)
+
+
+def rows_from_csv(graphs_csv, times_csv):
+    """The row list of a sweep kept as two CSV files (graph features; times),
+    the form the calibration sweep is committed in."""
+    import csv
+
+    def read(path):
+        with open(path) as f:
+            return list(csv.DictReader(line for line in f if not line.startswith("#")))
+    graphs = {g["config"]: g for g in read(graphs_csv)}
+    rows = []
+    for t in read(times_csv):
+        g = graphs[t["config"]]
+        rows.append({"config": t["config"], "N": int(t["N"]), "path": t["path"], "ms": float(t["ms"]),
+                     "gate_ok": t["gate_ok"] != "0", "M": int(g["M"]), "nnz": int(g["nnz"]),
+                     "d": float(g["d"]), "cv": float(g["cv"])})
+    return rows
 
 
 def evaluate(points, table="mi355x", near: float = 0.05):
@@ -115,12 +133,14 @@ def format_report(summary, rows, misses_only: bool = True) -> str:
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("sweep", nargs="+", help="JSON row lists written by bench.py --sweep-out")
+    ap.add_argument("sweep", nargs="*", help="JSON row lists written by bench.py --sweep-out")
+    ap.add_argument("--csv", nargs=2, metavar=("GRAPHS", "TIMES"), default=None,
+                    help="a sweep kept as two CSV files (graph features, times)")
     ap.add_argument("--table", default="mi355x", choices=sorted(TABLES))
     ap.add_argument("--all", action="store_true", help="list every point, not only misses")
     ap.add_argument("--output", default=None, help="write the per-point rows here (JSON)")
     args = ap.parse_args(argv)
-    rows = []
+    rows = rows_from_csv(*args.csv) if args.csv else []
     for path in args.sweep:
         with open(path) as f:
             rows += json.load(f)
