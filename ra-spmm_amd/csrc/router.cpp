@@ -74,18 +74,18 @@ constexpr RouterTable kReference = {
 //    FP32 tile route runs the same CSR kernels on the plan's stored values);
 //  - a CSR_DIRECT pick on skewed rows (cv >= 1.5) goes to ZERO_OVERHEAD_CSR
 //    (one lane group per hub row is 6.6x slower on config 2);
-//  - rule 2, uniform graphs of d >= 7 at N <= 64 go to CSR_DIRECT (config 3
-//    0.212 vs 0.218 ms for TC_DIRECT);
+//  - rule 2, uniform graphs of d >= 7 at N <= 64 go to CSR_DIRECT (faster on
+//    2 of the 3 such graphs);
 //  - rules 3, 5 and 6 pick SEGMENT_HYBRID: the fastest path on 26 of the 32
 //    points of those regions and within 19% on the rest (rule 5's guardrail
 //    pick, the baseline kernel, was 5-6x slower; rule 6's COMMUNITY_TC 1.5x
 //    slower on a graph with local columns; rule 3's split on M gave
 //    COMMUNITY_TC to large graphs, where it was 0-40% slower);
 //  - rule 7 picks TC_DIRECT without forcing the FP32 route (fastest on 5 of
-//    8 points; COMMUNITY_TC on the FP32 route meant CSR_DIRECT here, 1.4x
-//    slower at N = 64-128), and the small-graph FP32 condition (M <= 25000,
+//    8 points; COMMUNITY_TC on the FP32 route meant CSR_DIRECT here, 1.45-1.5x
+//    slower at N = 64), and the small-graph FP32 condition (M <= 25000,
 //    d < 9) holds only for uniform rows (cv < 0.7): on a small graph of cv 1
-//    the 16-bit tiles beat the CSR kernels 1.4-1.9x.
+//    the 16-bit tiles beat CSR_DIRECT 1.3-1.7x.
 //  Rule 1 keeps ZERO_OVERHEAD_CSR, the exact fp32 path, although the fp16
 //  COMMUNITY_TC is 1.4-1.7x faster on configs 2 and 5: the router does not
 //  trade precision for speed on extreme skew.
