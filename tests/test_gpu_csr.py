@@ -60,6 +60,22 @@ def test_csr_direct_and_baseline_bit_exact(oracle, M, K, d, skew, empty, N):
         np.testing.assert_array_equal(C.cpu().numpy(), ref, err_msg=fn.__name__)
 
 
+@pytest.mark.parametrize("M", [65535, 65536])
+@pytest.mark.parametrize("N", [256, 512])
+def test_csr_direct_xcd_slices_boundary(oracle, M, N):
+    """CSR_DIRECT deals 128-column slices to the XCDs when the unsliced grid
+    has fewer than 2^16 waves (one row per wave at N >= 256: M <= 65535), and
+    keeps whole rows above.  Both sides of the switch are the same fma chain
+    per element: bit-identical to the oracle."""
+    print(f"[csr slices] M={M} N={N}", flush=True)
+    g = S.random_csr(M, 20000, 4.0, seed=M + N, skew=1.1, empty_frac=0.02)
+    B = _B(g.K, N, seed=N + 1)
+    ref = oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B)
+    rp, ci, vl = _dev(g)
+    C = ra_spmm.spmm_csr_direct(rp, ci, vl, torch.from_numpy(B).cuda())
+    np.testing.assert_array_equal(C.cpu().numpy(), ref)
+
+
 def test_csr_direct_unaligned_B_uses_scalar_path(oracle):
     g = S.random_csr(500, 400, 8.0, seed=9)
     B = _B(400, 65, seed=3)

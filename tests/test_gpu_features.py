@@ -23,7 +23,9 @@ pytestmark = pytest.mark.gpu
 
 def _inputs():
     yield "ulp_case", _rowptr(ULP_CASE)
-    for seed, (M, d, skew) in enumerate([(1, 3.0, 0), (1000, 5.0, 1.0), (200_003, 12.0, 1.1)]):
+    # 65,536 rows is the largest matrix the one-block reduction takes
+    for seed, (M, d, skew) in enumerate([(1, 3.0, 0), (1000, 5.0, 1.0), (200_003, 12.0, 1.1),
+                                         (65_536, 6.0, 1.2), (65_537, 6.0, 1.2)]):
         yield f"random{seed}", S.random_csr(M, 5000, d, seed=seed, skew=skew, empty_frac=0.01).rowptr
     for (num, den), cv in EXACT:
         yield f"cv{cv}", exact_cv_rowptr(num, den, 1001, 37)
@@ -61,3 +63,25 @@ def test_feature_forms_against_oracle(oracle):
     print("cv32 ulp gap moment vs two-pass:", gaps, flush=True)
     assert max(gaps.values()) <= 1
     assert gaps["ulp_case"] == 1
+
+
+def test_feature_pass_behind_queued_work(oracle):
+    """The feature pass polls the result its kernel publishes and falls back to
+    a stream synchronisation after ~200 us: with ~tens of ms of SpMM queued
+    ahead of it on the same stream it takes the fallback, and the features are
+    the same as on an idle stream (both block sizes of the reduction)."""
+    big = S.CONFIGS["C2"]()
+    rp_b, ci_b, vl_b = big.torch("cuda")
+    B = torch.randn(big.K, 128, device="cuda")
+    for M in (10_000, 200_003):
+        rp = S.random_csr(M, 5000, 8.0, seed=M, skew=1.1).rowptr
+        want = oracle.features_gpu_reference(rp, M, M)
+        rpd = torch.from_numpy(rp).cuda()
+        torch.cuda.synchronize()
+        for _ in range(2):  # ~25 ms each: the baseline kernel on config C2
+            ra_spmm.spmm_csr_baseline(rp_b, ci_b, vl_b, B)
+        fd = ra_spmm.compute_features(rpd, M, M, 128)
+        assert (fd["nnz"], fd["avg_nnz_per_row"], fd["std_nnz_per_row"], fd["degree_cv"]) == \
+            (want[0], want[3], want[4], want[5])
+        idle = ra_spmm.compute_features(rpd, M, M, 128)
+        assert idle == fd
