@@ -95,6 +95,29 @@ constexpr RouterTable kMI355X = {
     1, 1.5f, 64, RA_PATH_SEGMENT_HYBRID, RA_PATH_SEGMENT_HYBRID, RA_PATH_SEGMENT_HYBRID,
     RA_PATH_TC_DIRECT, 0, 0.7f};
 
+// Decision reason of a rule whose path comes from the table: "<path>_<rule>".
+const char* table_reason(int p, int rule) {
+    static const char* const kReasons[4][5] = {
+        // CSR_DIRECT, ZERO_OVERHEAD_CSR, TC_DIRECT, COMMUNITY_TC, SEGMENT_HYBRID
+        {"csr_direct_skewed", "zero_overhead_skewed", "tc_direct_skewed", "community_tc_skewed",
+         "segment_hybrid_skewed"},
+        {"csr_direct_small_dense", "zero_overhead_small_dense", "tc_direct_small_dense",
+         "community_tc_small_dense", "segment_hybrid_small_dense_allN"},
+        {"csr_direct_heavy_mixed", "zero_overhead_heavy_mixed", "tc_direct_heavy_mixed",
+         "community_tc_heavy_mixed", "segment_hybrid_heavy_mixed"},
+        {"csr_direct_web_locality", "zero_overhead_web_locality", "tc_direct_web_locality",
+         "community_tc_web_locality", "segment_hybrid_web_locality"}};
+    const int r = rule == 3 ? 0 : rule == 5 ? 1 : rule == 6 ? 2 : 3;
+    switch (p) {
+        case RA_PATH_CSR_DIRECT: return kReasons[r][0];
+        case RA_PATH_ZERO_OVERHEAD_CSR: return kReasons[r][1];
+        case RA_PATH_TC_DIRECT: return kReasons[r][2];
+        case RA_PATH_COMMUNITY_TC: return kReasons[r][3];
+        case RA_PATH_SEGMENT_HYBRID: return kReasons[r][4];
+        default: return "table_path";
+    }
+}
+
 bool tile_family(int p) {
     return p == RA_PATH_TC_DIRECT || p == RA_PATH_COMMUNITY_TC || p == RA_PATH_SEGMENT_HYBRID;
 }
@@ -313,7 +336,7 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
     } else if (cv >= T.cv_skewed) {
         rule = 3;
         if (T.skewed_path >= 0) {
-            pick_table(T.skewed_path, "segment_hybrid_skewed");
+            pick_table(T.skewed_path, table_reason(T.skewed_path, 3));
         } else if (M >= T.m_skewed_large) {
             pick_tile(RA_PATH_COMMUNITY_TC, "community_tc_skewed_large", false);
         } else {
@@ -325,7 +348,7 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
     } else if (M < T.m_small && d >= T.d_small_dense) {
         rule = 5;
         if (T.small_dense_path >= 0) {
-            pick_table(T.small_dense_path, "segment_hybrid_small_dense_allN");
+            pick_table(T.small_dense_path, table_reason(T.small_dense_path, 5));
         } else if (N < T.n_small_narrow) {
             choice = RA_PATH_CUSPARSE;
             reason = "cusparse_small_dense_narrowN";
@@ -337,14 +360,11 @@ ra_status ra_route_dispatch(const ra_features* f, int32_t portfolio, int32_t tab
         }
     } else if (d >= T.d_heavy && cv >= T.cv_heavy) {
         rule = 6;
-        pick_tile(T.heavy_path, T.heavy_path == RA_PATH_COMMUNITY_TC ? "community_tc_heavy_mixed"
-                                                                     : "segment_hybrid_heavy_mixed",
-                  false);
+        pick_table(T.heavy_path, table_reason(T.heavy_path, 6));
     } else if (d < T.d_web && cv >= T.cv_web_lo && cv <= T.cv_web_hi && M >= T.m_web) {
         rule = 7;
-        pick_tile(T.web_path, T.web_path == RA_PATH_COMMUNITY_TC ? "community_tc_web_locality"
-                                                                 : "tc_direct_web_locality",
-                  T.web_fp32 != 0);
+        if (tile_family(T.web_path)) pick_tile(T.web_path, table_reason(T.web_path, 7), T.web_fp32 != 0);
+        else pick_table(T.web_path, table_reason(T.web_path, 7));
     } else {
         rule = 8;
         pick_tile(RA_PATH_TC_DIRECT, "tc_direct_default", false);

@@ -210,10 +210,11 @@ def route_with_rules(avg_nnz, degree_cv, M, N, nnz=None, *, disabled_rules=(), t
         else:
             choice, fp32 = pick("COMMUNITY_TC")
     elif 6 not in disabled and d >= _f32(T.d_heavy) and cv >= _f32(T.cv_heavy):
-        choice, fp32 = pick(T.heavy_path)
+        choice, fp32 = _direct(T.heavy_path)
     elif (7 not in disabled and d < _f32(T.d_web) and cv >= _f32(T.cv_web_lo)
           and cv <= _f32(T.cv_web_hi) and M >= T.m_web):
-        choice, fp32 = pick(T.web_path, T.web_fp32)
+        choice, fp32 = (pick(T.web_path, T.web_fp32) if T.web_path in ("TC_DIRECT", "COMMUNITY_TC", "SEGMENT_HYBRID")
+                        else (T.web_path, False))
     else:
         choice, fp32 = pick("TC_DIRECT")
 
