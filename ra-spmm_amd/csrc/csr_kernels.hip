@@ -14,7 +14,9 @@
 //                      than 256 write fp32 partials that a second launch sums
 //                      in ascending chunk order (deterministic, no atomics).
 //   features           exact integer degree moments (nnz, sum d^2, max d,
-//                      empty rows) in two deterministic launches.
+//                      empty rows): one launch up to 65,536 rows, two
+//                      deterministic launches above; the result goes to
+//                      mapped pinned host memory, which the host polls.
 //
 // Every output element of CSR_DIRECT, of the baseline and of ZO rows <= 256 is
 // one fp32 accumulator updated by fma in CSR order, which is bit-identical to
