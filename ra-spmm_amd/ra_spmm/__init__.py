@@ -27,11 +27,11 @@ from ._C import (  # noqa: F401
     spmm_csr_baseline_f16, spmm_csr_direct, spmm_cusparse,
 )
 from .dispatch import (  # noqa: F401
-    BASE_ATOL, COLD_ITERS, DEPLOYED_KERNELS, HARD_FAIL_THRESHOLD, TC_EXTRA_FACTOR, TILE_KERNELS, TIMED_ITERS,
+    BASE_ATOL, COLD_ITERS, COLD_ZO_MIN_CV, DEPLOYED_KERNELS, HARD_FAIL_THRESHOLD, TC_EXTRA_FACTOR, TILE_KERNELS, TIMED_ITERS,
     WARMUP, benchmark_cusparse, benchmark_cusparse_cold, benchmark_cusparse_fp16, benchmark_cusparse_fp16_cold,
-    benchmark_custom_cold, build_kernel_plan, correctness_gate, gpu_info_next, make_timing_breakdown,
+    benchmark_custom_cold, build_kernel_plan, cold_path, correctness_gate, gpu_info_next, make_timing_breakdown,
     measure_exec_ms, measure_ms, measure_one_ms, population_cv, run_kernel, run_oracle_cold, run_oracle_warm,
-    run_planned_kernel, run_router_cold, run_router_plan, run_router_warm, smallest_strict_crossover,
+    run_deployed_cold, run_planned_kernel, run_router_cold, run_router_plan, run_router_warm, smallest_strict_crossover,
     spmm_cusparse_fp16,
 )
 from .router import (  # noqa: F401

@@ -268,6 +268,38 @@ def run_router_plan(plan_dict, rowptr, colind, vals, B):
     return run_planned_kernel(label, plan, rowptr, colind, vals, B)
 
 
+# Degree CV from which the cold-aware policy runs ZERO_OVERHEAD_CSR (the MI355X
+# router table's zo_min_cv).
+COLD_ZO_MIN_CV = 1.5
+
+
+def cold_path(plan_dict) -> str:
+    """Path of the cold-aware policy for a single-call or streaming caller
+    (experiments/deployed_coldstart.py:1-10, gnn_bench/cold_first_step.py:61-139):
+    no tile-format build.  The reference runs CSR_DIRECT.  On MI355X a
+    ZERO_OVERHEAD_CSR plan is binned on the GPU from the device rowptr in
+    0.3-0.7 ms, while one lane group per hub row makes CSR_DIRECT 6.6x slower
+    on skewed rows (config C2: 6.6 against 1.0 ms), so rows of degree CV >= 1.5
+    take ZERO_OVERHEAD_CSR."""
+    cv = float(plan_dict["feature_values"]["degree_cv"])
+    return "ZERO_OVERHEAD_CSR" if cv >= COLD_ZO_MIN_CV else "CSR_DIRECT"
+
+
+def run_deployed_cold(rowptr, colind, vals, B, table="mi355x"):
+    """One cold call under the cold-aware policy, every overhead included: the
+    device feature pass and the rule tree, the policy's plan (a
+    ZERO_OVERHEAD_CSR binning from the device rowptr, or none) and the
+    execution.  Returns (C, label)."""
+    M = int(rowptr.numel()) - 1
+    K, N = int(B.shape[0]), int(B.shape[1])
+    plan_dict = _C.make_router_plan(rowptr, colind, vals, M, K, N, "MAIN", table)
+    label = cold_path(plan_dict)
+    if label == "ZERO_OVERHEAD_CSR":
+        plan = _C.make_zero_overhead_plan(rowptr, M, K)
+        return _C.run_zero_overhead_plan(plan, rowptr, colind, vals, B), label
+    return _C.spmm_csr_direct(rowptr, colind, vals, B), label
+
+
 def _router_generic(rowptr, colind, vals, B, portfolio, warmup, iters, cold, table="mi355x"):
     M = int(rowptr.numel()) - 1
     K, N = int(B.shape[0]), int(B.shape[1])

@@ -4,14 +4,16 @@ Reference: gnn_bench/router_vs_baselines_gcn.py — build_aggregation_operator
 (:89-126), GraphBackend (:162-410), validate_backend (:413-445),
 SparseMMFunction (:451-461), GCNBench (:464-476), measure_step (:482-498);
 cold first-step policy gnn_bench/cold_first_step.py:61-139 (route, then run
-CSR_DIRECT without building any plan).
+a path without a tile-format build).
 
 A GraphBackend owns the CSR of A and of A^T on the device, one router plan
 per (transpose, N) and one executor (path label + plan) per
 (backend, transpose, N).  Backends:
   "router"        MI355X router (default table), plan built on first use
   "router_cold"   first call per (transpose, N): feature pass + route, then
-                  CSR_DIRECT with no plan build; later calls as "router"
+                  the cold-aware policy's path (dispatch.cold_path: CSR_DIRECT,
+                  or ZERO_OVERHEAD_CSR binned on the GPU for skewed rows; no
+                  tile-format build); later calls as "router"
   "cusparse"      the guardrail name, served by the baseline CSR kernel
   "csr_direct", "zero_overhead", "tc_direct", "tc_direct_tf32",
   "community_tc", "segment_hybrid"   fixed paths
@@ -31,7 +33,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _C
-from .dispatch import BASE_ATOL, TC_EXTRA_FACTOR, TILE_KERNELS, build_kernel_plan, run_planned_kernel
+from .dispatch import BASE_ATOL, TC_EXTRA_FACTOR, TILE_KERNELS, build_kernel_plan, cold_path, run_planned_kernel
 from .router import route_label
 
 
@@ -127,6 +129,7 @@ class GraphBackend:
         self.exec_cache: Dict[Tuple[str, bool, int], tuple] = {}
         self._torch_sparse: Dict[bool, torch.Tensor] = {}
         self._cold_seen: set = set()
+        self._cold_zo: Dict[bool, object] = {}  # ZERO_OVERHEAD_CSR plans of cold first calls
 
     def _tensors(self, transpose: bool):
         return self.backward if transpose else self.forward
@@ -177,8 +180,8 @@ class GraphBackend:
                 # (a partial buffer that grows to the widest N) do not depend
                 # on N: share one plan per (family, transpose) across widths
                 # and precisions.
-                plan = None
-                if label in TILE_KERNELS or label == "ZERO_OVERHEAD_CSR":
+                plan = self._cold_zo.get(transpose) if label == "ZERO_OVERHEAD_CSR" else None
+                if plan is None and (label in TILE_KERNELS or label == "ZERO_OVERHEAD_CSR"):
                     fam = label.replace("_TF32", "")
                     for (b, tr, n), (lab, p) in self.exec_cache.items():
                         if tr == transpose and lab.replace("_TF32", "") == fam and p is not None:
@@ -195,11 +198,17 @@ class GraphBackend:
         t = self._tensors(transpose)
         ncols = int(B.shape[1])
         if backend == "router_cold" and (transpose, ncols) not in self._cold_seen:
-            # Cold first call: feature pass + route, then CSR_DIRECT, no plan build.
+            # Cold first call: feature pass + route, then the cold-aware
+            # policy's path, which builds no tile format.
             self._cold_seen.add((transpose, ncols))
-            self.get_router_plan(transpose, ncols)
-            return _C.spmm_csr_direct(t["rowptr"], t["colind"], t["vals"], B)
-        label, plan = self._get_executor(backend, transpose, ncols)
+            label, plan = cold_path(self.get_router_plan(transpose, ncols)), None
+            if label == "ZERO_OVERHEAD_CSR":
+                plan = self._cold_zo.get(transpose)
+                if plan is None:  # binned on the GPU from the device rowptr
+                    M = int(t["rowptr"].numel()) - 1
+                    plan = self._cold_zo[transpose] = _C.make_zero_overhead_plan(t["rowptr"], M, M)
+        else:
+            label, plan = self._get_executor(backend, transpose, ncols)
         if label == "CUSPARSE":
             return _C.run_cusparse_plan(plan, B).clone()
         if label == "rocsparse":

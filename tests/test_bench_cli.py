@@ -49,12 +49,17 @@ def test_block_of_carries_the_driver_fields():
            "max_rel_err_vs_baseline": 3e-7, "rocsparse": {"ms": 1.5, "alg": "csr_nnz_split"},
            "speedup_vs_rocsparse": 1.5, "torch_sparse_gpu": {"ms": 30.0}, "speedup_vs_torch_sparse_gpu": 30.0,
            "cpu_torch_sparse": {"value": 33.0, "sample": "full matrix"},
-           "gather_ceiling": {"csr_order": {"ms": 0.81}, "uniform": {"ms": 1.1}}}
+           "gather_ceiling": {"csr_order": {"ms": 0.81}, "uniform": {"ms": 1.1}},
+           "cold_speedup_vs_rocsparse": 0.9,
+           "deployed_cold": {"path": "ZERO_OVERHEAD_CSR", "ms": 2.0, "speedup_vs_rocsparse": 0.8}}
+    res["rocsparse"]["cold_ms"] = 1.6
     b = bench.block_of(res)
     assert b["roofline"]["frac"] == round(1e9 / 0.9e-3 / 1e9 / 8000.0, 4)
     assert b["roofline"]["frac_of_gather_probe"] == round(0.81 / 0.9, 4)
     assert b["speedup_vs_rocsparse"] == 1.5 and b["rocsparse_alg"] == "csr_nnz_split"
-    assert set(b["cold"]) == {"route_ms", "build_ms", "first_exec_ms"}
+    assert set(b["cold"]) == {"route_ms", "build_ms", "first_exec_ms", "rocsparse_cold_ms", "speedup_vs_rocsparse",
+                              "deployed_path", "deployed_ms", "deployed_speedup_vs_rocsparse"}
+    assert b["cold"]["deployed_speedup_vs_rocsparse"] == 0.8 and b["cold"]["rocsparse_cold_ms"] == 1.6
     # a tile plan's probe walks its vector columns and is keyed plan_order
     res["gather_ceiling"] = {"plan_order": {"ms": 0.45, "gathers": 10}}
     assert bench.block_of(res)["roofline"]["frac_of_gather_probe"] == round(0.45 / 0.9, 4)

@@ -300,3 +300,25 @@ def test_harness_helpers_run_every_deployed_kernel(oracle):
             assert cold["cold_exec_ms"] > 0 and (cold["preprocess_ms"] > 0) == (k != "CSR_DIRECT")
     assert len(cache) == len(ra_spmm.DEPLOYED_KERNELS) + 1
     assert ra_spmm.measure_ms(lambda: ra_spmm.spmm_csr_direct(rp, ci, vl, B), 2, 5) > 0
+
+
+def test_deployed_cold_policy(oracle):
+    """The cold-aware single-call policy (run_deployed_cold): uniform rows run
+    CSR_DIRECT, bit-identical to the oracle; skewed rows (degree CV >= 1.5) run
+    ZERO_OVERHEAD_CSR binned from the device rowptr, equal to a ZO plan built
+    from the host rowptr."""
+    N = 64
+    uni = S.random_csr(3000, 2000, 9.0, seed=21)
+    skew = S.random_csr(3000, 2000, 9.0, seed=22, skew=0.9)
+    for g, want in ((uni, "CSR_DIRECT"), (skew, "ZERO_OVERHEAD_CSR")):
+        rp, ci, vl = _dev(g)
+        B = _B(g.K, N, seed=5)
+        Bd = torch.from_numpy(B).cuda()
+        C, label = ra_spmm.run_deployed_cold(rp, ci, vl, Bd)
+        cv = ra_spmm.make_router_plan(rp, ci, vl, g.M, g.K, N)["feature_values"]["degree_cv"]
+        assert label == want and (cv >= ra_spmm.COLD_ZO_MIN_CV) == (want == "ZERO_OVERHEAD_CSR"), (label, cv)
+        if want == "CSR_DIRECT":
+            np.testing.assert_array_equal(C.cpu().numpy(), oracle.spmm_seq_f32(g.rowptr, g.colind, g.vals, B))
+        else:
+            host = ra_spmm.make_zero_overhead_plan(rp.cpu(), g.M, g.K)
+            assert torch.equal(C, ra_spmm.run_zero_overhead_plan(host, rp, ci, vl, Bd))
