@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <mutex>
 #include <string>
 
 #include "ra_internal.hpp"
@@ -129,6 +130,11 @@ __global__ void zero_flags(unsigned* flags) {
     if (threadIdx.x < 2) flags[threadIdx.x] = 0u;
 }
 
+constexpr size_t kCachedTmpBytes = size_t(256) << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_tmp_mutex;
+ra::DeviceBuffer* g_tmp[kMaxDevices] = {};
+
 unsigned grid_for(int64_t n) {
     return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, 1 << 16)));
 }
@@ -145,9 +151,25 @@ ra_status gpu_bin(ra_zo_plan* p, const int32_t* rowptr, int32_t M, int32_t K, hi
     RA_HIP_TRY(hipcub::DeviceScan::ExclusiveScan(nullptr, scan_bytes, cnull, cnull, ZoCountsSum(), ZoCounts{},
                                                  M + 1, st));
     const size_t counts_bytes = ((size_t)(M + 1) * sizeof(ZoCounts) + 255) & ~size_t(255);
-    ra::DeviceBuffer tmp;
     const unsigned cgrid = grid_for(M + 1);
-    RA_TRY(tmp.allocate(2 * counts_bytes + ((scan_bytes + 255) & ~size_t(255)) + 256 + (size_t)cgrid * sizeof(unsigned)));
+    const size_t tmp_bytes =
+        2 * counts_bytes + ((scan_bytes + 255) & ~size_t(255)) + 256 + (size_t)cgrid * sizeof(unsigned);
+    // The counters come from a per-device buffer kept for the process (up to
+    // kCachedTmpBytes; a hipMalloc + hipFree pair costs a cold build
+    // ~0.3 ms); larger builds allocate their own.  Builds on one device are
+    // serialised by the buffer's lock.
+    ra::DeviceBuffer own;
+    std::unique_lock<std::mutex> lock;
+    ra::DeviceBuffer* tmpp = &own;
+    if (tmp_bytes <= kCachedTmpBytes && p->device >= 0 && p->device < kMaxDevices) {
+        lock = std::unique_lock<std::mutex>(g_tmp_mutex);
+        if (!g_tmp[p->device]) g_tmp[p->device] = new ra::DeviceBuffer();  // kept until exit
+        tmpp = g_tmp[p->device];
+        RA_TRY(tmpp->ensure(tmp_bytes));
+    } else {
+        RA_TRY(own.allocate(tmp_bytes));
+    }
+    ra::DeviceBuffer& tmp = *tmpp;
     ZoCounts* counts = tmp.get<ZoCounts>();
     ZoCounts* pre = reinterpret_cast<ZoCounts*>(tmp.get<char>() + counts_bytes);
     void* scan_tmp = tmp.get<char>() + 2 * counts_bytes;
