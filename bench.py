@@ -609,23 +609,39 @@ def profile_traffic(kernel: str, cfg: str, N: int):
 
 
 def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocsparse", "cusparse", "zero_overhead",
-                                              "csr_direct"), order_auto=True):
-    """config C5: 2-layer GCN training step (128 -> 256 -> 47) on the
-    synthetic power-law operator, forward A X and backward A^T G routed per
-    (transpose, N).  Reports step time per backend and the routed paths."""
+                                              "csr_direct"), order_auto=True, model="gcn"):
+    """config C5: 2-layer GNN training step (128 -> 256 -> 47) on the
+    synthetic power-law graph, forward A X and backward A^T G routed per
+    (transpose, N).  model "gcn" (the config) runs on C5's GCN operator;
+    "sage" and "gin" (gnn_bench/router_vs_baselines_{sage,gin}.py) on the same
+    graph's mean and raw-sum operators.  Reports step time per backend and
+    the routed paths."""
     import numpy as np
     import scipy.sparse as sp
     import torch
     from ra_spmm import gnn
     from ra_spmm import synthetic as S
     S.use_device_sort("cuda")
-    g = S.CONFIGS["C5"]()
-    op = sp.csr_matrix((g.vals, g.colind, g.rowptr), shape=(g.M, g.M))
+    if model == "gcn":
+        g = S.CONFIGS["C5"]()
+        op = sp.csr_matrix((g.vals, g.colind, g.rowptr), shape=(g.M, g.M))
+    else:
+        base = S.chung_lu(1_000_000, 25.0, 2.3, 50_000, seed=5)  # C5's graph before normalisation
+        adj = sp.csr_matrix((np.ones(base.nnz, np.float32), base.colind, base.rowptr), shape=(base.M, base.M))
+        op = gnn.build_aggregation_operator(adj, model)
+        g = S.Graph(op.indptr.astype(np.int32), op.indices.astype(np.int32), op.data.astype(np.float32),
+                    op.shape[0], op.shape[1], f"{model}_{base.name}")
+        order_auto = False
+    cls = gnn.MODELS[model]
     torch.manual_seed(0)
     X = torch.randn(g.M, 128, device="cuda")
     y = torch.randint(0, 47, (g.M,), device="cuda")
-    out = {"graph": g.name, "M": g.M, "nnz": g.nnz, "in": 128, "hidden": 256, "classes": 47,
-           "spmm_flops_per_step": 2.0 * g.nnz * (256 + 47) * 2}
+    widths = {"gcn": (256, 47), "sage": (128, 256), "graphsage": (128, 256), "gin": (128, 256)}[model]
+    # forward SpMMs at both widths, backward A^T SpMMs where the operand takes a
+    # gradient (every GCN layer; SAGE and GIN: not X)
+    n_bwd = widths if model == "gcn" else widths[1:]
+    out = {"model": model, "graph": g.name, "M": g.M, "nnz": g.nnz, "in": 128, "hidden": 256, "classes": 47,
+           "spmm_flops_per_step": 2.0 * g.nnz * (sum(widths) + sum(n_bwd))}
     # Load the dense (GEMM, softmax, Adam) kernels once, so that the first
     # backend's cold step measures routing and plan builds, not library start-up.
     warm = gnn.GCN(128, 256, 47).cuda()
@@ -634,6 +650,7 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
         wopt.zero_grad(set_to_none=True)
         gnn.cross_entropy(warm.lin2(torch.relu(warm.lin1(X)))[:, :47], y).backward()
         wopt.step()
+    widths_val = (256, 47) if model == "gcn" else (128, 256)
     torch.cuda.synchronize()
     del warm, wopt
     for backend in backends:
@@ -641,20 +658,18 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
         # the reference does (gnn_bench/router_vs_baselines_gcn.py:413-446,
         # 566-567): each (transpose, N) SpMM of the step, N = 256 and 47,
         # against the baseline kernel with the harness's gate.
-        val = gnn.validate_backend(op, "cuda", backend, (256, 47), seed=0, table=table)
+        val = gnn.validate_backend(op, "cuda", backend, widths_val, seed=0, table=table)
         torch.cuda.empty_cache()
         log(f"[gcn] {backend:14s} validation: correct={val['correct']} max_error={val['max_error']:.3e} "
             f"tolerance={val['tolerance']:.3e}")
         torch.manual_seed(1)
         graph = gnn.GraphBackend(op, "cuda", table)
-        model = gnn.GCN(128, 256, 47).cuda()
-        opt = torch.optim.Adam(model.parameters(), lr=1e-2)
-        t0 = time.perf_counter()
-        cold = gnn.train_step(model, graph, backend, X, y, opt)
-        setup = time.perf_counter() - t0
+        net = cls(128, 256, 47).cuda()
+        opt = torch.optim.Adam(net.parameters(), lr=1e-2)
+        cold = gnn.train_step(net, graph, backend, X, y, opt)
         for _ in range(warmup):
-            gnn.train_step(model, graph, backend, X, y, opt)
-        ts = [gnn.train_step(model, graph, backend, X, y, opt) for _ in range(steps)]
+            gnn.train_step(net, graph, backend, X, y, opt)
+        ts = [gnn.train_step(net, graph, backend, X, y, opt) for _ in range(steps)]
         ms = 1e3 * sum(ts) / len(ts)
         rec = {"step_ms": ms, "cold_first_step_ms": cold * 1e3,
                "validation": {k: val[k] for k in ("correct", "max_error", "tolerance")}}
@@ -664,7 +679,7 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
         out[backend] = rec
         log(f"[gcn] {backend:14s} step {ms:8.3f} ms  cold first step {cold * 1e3:9.1f} ms "
             f"{rec.get('paths', '')}")
-        del graph, model, opt
+        del graph, net, opt
         torch.cuda.empty_cache()
     if "router" in backends and order_auto:
         # The same model with order="auto": layer 1 aggregates before its
@@ -672,17 +687,17 @@ def bench_gcn(steps, warmup, table, backends=("router", "router_cold", "rocspars
         # reference-order step, never in its place.
         torch.manual_seed(1)
         graph = gnn.GraphBackend(op, "cuda", table)
-        model = gnn.GCN(128, 256, 47, order="auto").cuda()
-        opt = torch.optim.Adam(model.parameters(), lr=1e-2)
-        cold = gnn.train_step(model, graph, "router", X, y, opt)
+        net = gnn.GCN(128, 256, 47, order="auto").cuda()
+        opt = torch.optim.Adam(net.parameters(), lr=1e-2)
+        cold = gnn.train_step(net, graph, "router", X, y, opt)
         for _ in range(warmup):
-            gnn.train_step(model, graph, "router", X, y, opt)
-        ts = [gnn.train_step(model, graph, "router", X, y, opt) for _ in range(steps)]
+            gnn.train_step(net, graph, "router", X, y, opt)
+        ts = [gnn.train_step(net, graph, "router", X, y, opt) for _ in range(steps)]
         ms = 1e3 * sum(ts) / len(ts)
         out["router_order_auto"] = {"step_ms": ms, "cold_first_step_ms": cold * 1e3,
                                     "spmm_flops_per_step": 2.0 * g.nnz * (128 + 47 + 47)}
         log(f"[gcn] router order=auto step {ms:8.3f} ms  cold first step {cold * 1e3:9.1f} ms")
-        del graph, model, opt
+        del graph, net, opt
         torch.cuda.empty_cache()
     return out
 
@@ -948,6 +963,8 @@ def main(argv=None):
                     help="cold routing cost (make_router_plan) broken down on C1 and C2")
     ap.add_argument("--copy-probe", action="store_true", help="run a 1 GiB copy first (PMC scale)")
     ap.add_argument("--gcn", action="store_true", help="config 5 GCN training step (details on stderr)")
+    ap.add_argument("--gnn-model", default="gcn", choices=["gcn", "sage", "gin"],
+                    help="model of --gcn: the config's GCN, or GraphSAGE / GIN on the same graph")
     ap.add_argument("--gcn-backends", default="router,router_cold,rocsparse,cusparse,zero_overhead,csr_direct",
                     help="comma-separated GraphBackend backends timed by --gcn")
     args = ap.parse_args(argv)
@@ -967,7 +984,7 @@ def main(argv=None):
     import ra_spmm
     if args.gcn:
         res = bench_gcn(max(5, args.steps // 20), max(2, args.warmup // 10), args.table,
-                        tuple(args.gcn_backends.split(",")))
+                        tuple(args.gcn_backends.split(",")), model=args.gnn_model)
         if args.details:
             Path(args.details).parent.mkdir(parents=True, exist_ok=True)
             Path(args.details).write_text(json.dumps(res, indent=1))

@@ -3,6 +3,8 @@
 Reference: gnn_bench/router_vs_baselines_gcn.py — build_aggregation_operator
 (:89-126), GraphBackend (:162-410), validate_backend (:413-445),
 SparseMMFunction (:451-461), GCNBench (:464-476), measure_step (:482-498);
+SAGEBench gnn_bench/router_vs_baselines_sage.py:48-67; GINBench
+gnn_bench/router_vs_baselines_gin.py:47-73;
 cold first-step policy gnn_bench/cold_first_step.py:61-139 (route, then run
 a path without a tile-format build).
 
@@ -369,6 +371,59 @@ class GCN(nn.Module):
 
 
 GCNBench = GCN
+
+
+class SAGE(nn.Module):
+    """2-layer GraphSAGE with the mean aggregator, full batch
+    (gnn_bench/router_vs_baselines_sage.py:48-67): per layer
+    h' = W [h, A h], with A = D^-1 A_raw (build_aggregation_operator(..., "sage"),
+    no self-loops: the self term is the concatenated h).  Two routed SpMMs per
+    forward, at the input and the hidden width; the first needs no backward
+    SpMM (X takes no gradient).  Bias-free linear maps as in the reference,
+    with the chunked weight gradient of ``Linear``."""
+
+    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int):
+        super().__init__()
+        self.lin1 = Linear(2 * in_dim, hidden_dim)
+        self.lin2 = Linear(2 * hidden_dim, out_dim)
+
+    def forward(self, X, graph: GraphBackend, backend: str):
+        h = F.relu(self.lin1(torch.cat([X, SparseMMFunction.apply(X, graph, backend)], dim=1)))
+        h = h[:, :self.lin1.out_features]
+        out = self.lin2(torch.cat([h, SparseMMFunction.apply(h, graph, backend)], dim=1))
+        return out[:, :self.lin2.out_features]
+
+
+class GIN(nn.Module):
+    """2-layer GIN (gnn_bench/router_vs_baselines_gin.py:47-73): per layer
+    h' = MLP((1 + eps) h + A h) with A the raw adjacency
+    (build_aggregation_operator(..., "gin")), a learnable eps per layer
+    (initialised to 0) and 2-layer bias-free MLPs (in -> hidden -> hidden,
+    hidden -> hidden -> out), ReLU between the layers."""
+
+    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int):
+        super().__init__()
+        self.eps1 = nn.Parameter(torch.zeros(1))
+        self.eps2 = nn.Parameter(torch.zeros(1))
+        self.mlp1 = nn.ModuleList([Linear(in_dim, hidden_dim), Linear(hidden_dim, hidden_dim)])
+        self.mlp2 = nn.ModuleList([Linear(hidden_dim, hidden_dim), Linear(hidden_dim, out_dim)])
+
+    @staticmethod
+    def _mlp(layers, h):
+        a, b = layers
+        h = F.relu(a(h)[:, :a.out_features])
+        return b(h)[:, :b.out_features]
+
+    def forward(self, X, graph: GraphBackend, backend: str):
+        h = (1.0 + self.eps1) * X + SparseMMFunction.apply(X, graph, backend)
+        h = F.relu(self._mlp(self.mlp1, h))
+        h = (1.0 + self.eps2) * h + SparseMMFunction.apply(h.contiguous(), graph, backend)
+        return self._mlp(self.mlp2, h)
+
+
+SAGEBench = SAGE
+GINBench = GIN
+MODELS = {"gcn": GCN, "sage": SAGE, "graphsage": SAGE, "gin": GIN}
 
 
 def cross_entropy(logits: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
