@@ -143,7 +143,10 @@ typedef struct ra_features {
 
 ra_status ra_features_host(const int32_t* h_rowptr, int32_t M, int32_t K, int32_t N,
                            ra_features* out);
-/* Synchronises `stream` (one 32-byte readback). */
+/* Returns once the result is on the host: the reduction's last kernel writes
+ * it to mapped pinned memory, which the call polls, falling back to a
+ * synchronisation of `stream` after ~200 us (work queued ahead, or an error).
+ * Calls are serialised per process (per-device buffers); not capturable. */
 ra_status ra_features_device(const int32_t* d_rowptr, int32_t M, int32_t K, int32_t N,
                              ra_stream_t stream, ra_features* out);
 /* Diagnostic ("FULL") structural features of a CSR matrix: row-length skew,
