@@ -859,7 +859,7 @@ def sweep(configs, Ns, steps, out_path):
     rows = []
     for cfg in configs:
         S.use_device_sort("cuda")
-        g = S.CONFIGS[cfg]() if cfg in S.CONFIGS else S.REGIMES[cfg]()
+        g = S.CONFIGS[cfg]() if cfg in S.CONFIGS else S.REGIMES[cfg]() if cfg in S.REGIMES else S.HELDOUT[cfg]()
         feat = production_features(g.rowptr)
         rp, ci, vl = g.torch("cuda")
         host = (rp.cpu(), ci.cpu(), vl.cpu())  # plan builders take host CSR, as in the reference
@@ -949,8 +949,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--traffic", type=float, default=None,
                     help="HBM bytes per launch of the dominant kernel from rocprofv3 --pmc")
-    ap.add_argument("--sweep", default=None, help="comma-separated configs (C1..C5, regime names, or 'regimes' for the "
-                         "router calibration suite) to sweep all paths on")
+    ap.add_argument("--sweep", default=None, help="comma-separated configs (C1..C5, regime names, 'regimes' for the router "
+                         "calibration suite, 'heldout' for its held-out graphs) to sweep all paths on")
     ap.add_argument("--sweep-N", default="64,128,256")
     ap.add_argument("--sweep-out", default=None, help="write the sweep rows here as JSON")
     ap.add_argument("--details", default=None, help="write the full result dict here")
@@ -1001,9 +1001,9 @@ def main(argv=None):
     if args.sweep:
         names = []
         for n in args.sweep.split(","):
-            if n == "regimes":  # the router calibration suite
+            if n in ("regimes", "heldout"):  # the router calibration suite / its held-out graphs
                 from ra_spmm import synthetic as S
-                names += list(S.REGIMES)
+                names += list(S.REGIMES if n == "regimes" else S.HELDOUT)
             else:
                 names.append(n)
         sweep(names, [int(n) for n in args.sweep_N.split(",")], max(10, args.steps // 4),

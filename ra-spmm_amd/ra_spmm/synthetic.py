@@ -325,6 +325,25 @@ REGIMES = {
 }
 
 
+# Held-out graphs for the router calibration: the same generators with other
+# sizes, degrees, skews, localities and seeds, never used to set a knob; they
+# check that the MI355X table carries beyond the suite it was set on
+# (the reference's unseen-graph validation, experiments/unseen_validation.py).
+HELDOUT = {
+    "H1_extreme_small": lambda: chung_lu(60_000, 10.0, 2.05, 8_000, seed=41),
+    "H2_uniform_mid": lambda: er(250_000, 24.0, seed=42),
+    "H2_lowd_banded": lambda: regime_graph(700_000, 3.5, 0.45, 0.9, 128, seed=43, name="H2_lowd_banded"),
+    "H3_skewed_pop": lambda: regime_graph(350_000, 15.0, 3.6, popular=True, seed=44, name="H3_skewed_pop"),
+    "H4_dense_skew": lambda: regime_graph(80_000, 120.0, 1.6, 0.3, 512, popular=True, seed=45,
+                                          name="H4_dense_skew"),
+    "H5_small_dense": lambda: regime_graph(12_000, 32.0, 0.8, 0.5, 256, seed=46, name="H5_small_dense"),
+    "H6_heavy": lambda: regime_graph(150_000, 35.0, 2.6, 0.2, 256, popular=True, seed=47, name="H6_heavy"),
+    "H7_web": lambda: regime_graph(400_000, 7.0, 1.25, 0.6, 512, seed=48, name="H7_web"),
+    "H8_mid_local": lambda: regime_graph(250_000, 16.0, 1.5, 0.6, 2048, seed=49, name="H8_mid_local"),
+    "H8_small_skew": lambda: regime_graph(15_000, 6.0, 1.8, seed=50, name="H8_small_skew"),
+}
+
+
 CONFIGS = {
     "C1": lambda: er(10_000, 8.0, seed=1),
     "C2": lambda: chung_lu(1_000_000, 16.0, 2.1, 50_000, seed=2),

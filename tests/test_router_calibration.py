@@ -77,3 +77,15 @@ def test_rule_regions_winners(points):
         if _rule(p) == 5 and N < 96:
             t = p["times"]
             assert 5.0 <= t["CUSPARSE"] / min(t.values()) <= 6.5, (g, N)
+
+
+def test_mi355x_table_on_held_out_graphs():
+    """Ten held-out graphs (synthetic.HELDOUT: other sizes, degrees, skews,
+    localities and seeds, one or more per region), never used to set a knob:
+    the MI355X table keeps its advantage over the published thresholds."""
+    pts = points_from_sweep(rows_from_csv(GOLD / "router_heldout_graphs.csv", GOLD / "router_heldout_times.csv"))
+    assert len(pts) == 40
+    mi, _ = evaluate(pts, "mi355x")
+    ref, _ = evaluate(pts, "reference")
+    assert (mi["hits"], mi["near_hits"]) == (17, 30) and (ref["hits"], ref["near_hits"]) == (8, 19)
+    assert round(mi["router_oracle_geomean"], 3) == 0.951 and round(ref["router_oracle_geomean"], 3) == 0.846
