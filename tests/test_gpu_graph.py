@@ -12,7 +12,8 @@ pytestmark = pytest.mark.gpu
 import ra_spmm  # noqa: E402
 from ra_spmm import synthetic as S  # noqa: E402
 
-CASES = [("CSR_DIRECT", 64), ("ZERO_OVERHEAD_CSR", 128), ("TC_DIRECT", 128), ("COMMUNITY_TC", 96),
+CASES = [("CSR_DIRECT", 64), ("CSR_DIRECT", 256),  # 256: XCD-dealt column slices (small matrix)
+         ("ZERO_OVERHEAD_CSR", 128), ("ZERO_OVERHEAD_CSR", 512), ("TC_DIRECT", 128), ("COMMUNITY_TC", 96),
          ("SEGMENT_HYBRID", 64), ("TC_DIRECT_TF32", 64), ("SEGMENT_HYBRID_TF32", 48)]
 
 
