@@ -86,9 +86,11 @@ constexpr RouterTable kReference = {
 //    slower at N = 64), and the small-graph FP32 condition (M <= 25000,
 //    d < 9) holds only for uniform rows (cv < 0.7): on a small graph of cv 1
 //    the 16-bit tiles beat CSR_DIRECT 1.3-1.7x.
-//  Rule 1 keeps ZERO_OVERHEAD_CSR, the exact fp32 path, although the fp16
-//  COMMUNITY_TC is 1.4-1.7x faster on configs 2 and 5: the router does not
-//  trade precision for speed on extreme skew.
+//  Rule 1 keeps the reference's pick, ZERO_OVERHEAD_CSR (the exact fp32
+//  path), although the 16-bit COMMUNITY_TC is 1.3-1.7x faster there and
+//  passes the harness's gate: the rule carries the fp32 benchmark configs 2
+//  and 5, and the bf16x3 split that would keep ~2^-16 accuracy measured
+//  slower than ZERO_OVERHEAD_CSR.
 constexpr RouterTable kMI355X = {
     5.0f, 0.7f, 4.5f, 256, 0.2f, 7.0f, 128, 3.0f, 250000, 40.0f, 20000, 25.0f, 96, 256,
     25.0f, 1.8f, 9.0f, 1.10f, 1.45f, 250000, 1.5f, 1e-9, 20.0, 5.0f, 25000, 9.0f,
